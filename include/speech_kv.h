@@ -1,0 +1,182 @@
+/*
+ * speech_kv.h — C ABI of the MI355X (gfx950) decoder KV-cache hot path.
+ *
+ * One shared library (libspeechkv.so) exports these entry points. They replace
+ * the PyTorch tensor ops the reference engine runs on its decoder KV-cache path:
+ *
+ *   skv_append            paged KV append (slot_mapping scatter into BlockManager
+ *                         blocks). Replaces `key_pool[l][blk, off] = new_k` at
+ *                         speech_serving/phase_aware_scheduler.py:1001-1010 and the
+ *                         prefill write at :678-690 (graph analogue: the scatter_ at
+ *                         speech_serving/models.py:449-454; TTS: tts_engine.py:197-204).
+ *   skv_gather            block-table gather into a zero-padded contiguous batch.
+ *                         Replaces `pool[l][table].view(-1,H,D)[:T].permute(1,0,2)`
+ *                         at speech_serving/tts_engine.py:177-185,
+ *                         speech_serving/encoder_attention.py:50-59 and
+ *                         speech_serving/phase_aware_scheduler.py:617-623, 860-882,
+ *                         plus the zero-padded batching at :818-830.
+ *   skv_paged_attention   fused paged self-attention decode over the block table.
+ *                         Replaces matmul/mask/softmax/matmul at
+ *                         speech_serving/models.py:126-165 (eager) and :444-466
+ *                         (graph) together with the working-KV cat/pad at
+ *                         speech_serving/phase_aware_scheduler.py:795-846,1012-1018.
+ *                         Same computation as the Triton kernel at
+ *                         scripts/evaluate_paging_variants.py:56-133.
+ *   skv_dense_attention   attention over contiguous K/V with per-row valid length
+ *                         (cross-attention against the encoder K/V handed off by
+ *                         graph_direct_encoder_kv, and causal prompt attention over
+ *                         contiguous K/V). Replaces speech_serving/models.py:167-203
+ *                         (eager) and :468-479 (graph), with the masks of
+ *                         phase_aware_scheduler.py:884-887,964-970 and
+ *                         graph_decode_buffers.py:529,537 expressed as lengths.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer owned by the caller (PyTorch).
+ *     The library never allocates, frees or synchronises; every launch is
+ *     ordered on `stream` (a hipStream_t; NULL = the null stream) and is safe to
+ *     record into a HIP graph.
+ *   - Strides are in elements of the tensor's dtype. The innermost (head_dim)
+ *     dimension must be contiguous, and every row start must be 16-byte aligned.
+ *   - dtype codes: SKV_F32, SKV_F16, SKV_BF16. K/V, Q and the output share one dtype.
+ *   - Return value: SKV_OK (0) on success, a negative SKV_E* code for an invalid
+ *     argument, or a positive hipError_t from the launch. skv_last_error() gives
+ *     a message for the last failing call on the calling thread.
+ *   - Index robustness: rows whose slot (append) or block id (gather, attention)
+ *     is negative or >= the pool size are skipped (append), zero-filled (gather) or
+ *     excluded from the softmax (attention); no out-of-bounds access is made.
+ */
+#ifndef SPEECH_KV_H_
+#define SPEECH_KV_H_
+
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define SKV_API __attribute__((visibility("default")))
+#else
+#define SKV_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum skv_dtype { SKV_F32 = 0, SKV_F16 = 1, SKV_BF16 = 2 };
+
+enum skv_status {
+  SKV_OK = 0,
+  SKV_EINVAL = -1,     /* bad size / null pointer / unsupported head_dim */
+  SKV_EDTYPE = -2,     /* unknown dtype code */
+  SKV_EALIGN = -3,     /* pointer or stride not 16-byte aligned */
+  SKV_EWORKSPACE = -4  /* split-K partials or counters missing / too small */
+};
+
+/* Library version string, e.g. "speechkv 0.1.0 gfx950". */
+SKV_API const char* skv_version(void);
+
+/* Message describing the last non-OK return on the calling thread. */
+SKV_API const char* skv_last_error(void);
+
+/*
+ * skv_append — scatter N new token rows of K and V into the paged pools.
+ *   k_new, v_new : [N, H, D] rows (row stride new_stride_n, head stride new_stride_h)
+ *   k_pool,v_pool: [num_blocks, block_size, H, D], contiguous
+ *   slot_mapping : int64 [N] device; slot = block_id * block_size + offset;
+ *                  a negative slot skips that row.
+ * Either v_new/v_pool pair may be NULL to append K only.
+ * Reference: phase_aware_scheduler.py:1004-1010 (decode), :681-690 (prefill).
+ */
+SKV_API int skv_append(const void* k_new, const void* v_new,
+               int64_t new_stride_n, int64_t new_stride_h,
+               void* k_pool, void* v_pool,
+               const int64_t* slot_mapping,
+               int32_t n_tokens, int32_t num_heads, int32_t head_dim,
+               int64_t num_slots, int32_t dtype, void* stream);
+
+/*
+ * skv_gather — materialise paged K/V as a zero-padded contiguous batch.
+ *   block_tables : int32 [B, table_stride] device
+ *   lens         : int32 [B] device, valid tokens per row (<= max_len)
+ *   k_out, v_out : [B, H, max_len, D] contiguous; positions >= lens[b] are zeroed.
+ * v_pool/v_out may be NULL to gather K only.
+ * Reference: tts_engine.py:177-185; phase_aware_scheduler.py:617-623, 818-830.
+ */
+SKV_API int skv_gather(const void* k_pool, const void* v_pool,
+               const int32_t* block_tables, int32_t table_stride,
+               const int32_t* lens,
+               void* k_out, void* v_out,
+               int32_t batch, int32_t num_heads, int32_t head_dim,
+               int32_t block_size, int32_t num_blocks, int32_t max_len,
+               int32_t dtype, void* stream);
+
+/*
+ * Split-K scratch for skv_paged_attention / skv_dense_attention. A call with
+ * `rows` = batch * q_len query rows and `num_heads` heads whose keys span more
+ * than one chunk of `chunk_tokens` (0 = library default for `dtype`) needs:
+ *   partials : skv_attention_workspace_bytes(...) bytes, 16-byte aligned, any content;
+ *   counters : int32 [rows * num_heads] arrival counters that are zero before
+ *              the call; every call leaves them zero again. Keep the counter
+ *              buffer for counters only (never reuse it as partials), so it
+ *              stays zero between calls and across HIP-graph replays.
+ * skv_attention_workspace_bytes returns 0 when every row fits one chunk (then
+ * both pointers may be NULL).
+ */
+SKV_API int64_t skv_attention_workspace_bytes(int32_t rows, int32_t num_heads, int32_t head_dim,
+                                      int32_t max_len, int32_t chunk_tokens, int32_t dtype);
+
+/* Chunk size the library uses when chunk_tokens == 0. */
+SKV_API int32_t skv_default_chunk_tokens(int32_t rows, int32_t num_heads, int32_t head_dim,
+                                 int32_t max_len, int32_t dtype);
+
+/*
+ * skv_paged_attention — softmax(q K^T * scale) V over the paged K/V of each row.
+ *   q   : [B, Q, H, D] with strides (q_stride_b, q_stride_q, q_stride_h)
+ *   out : [B, Q, H, D] with strides (o_stride_b, o_stride_q, o_stride_h)
+ *   k_pool, v_pool : [num_blocks, block_size, num_kv_heads, D] contiguous
+ *   block_tables   : int32 [*, table_stride]; row b uses table row
+ *                    table_rows ? table_rows[b] : b
+ *   ctx_lens : int32 [B] keys visible to the LAST query of row b (new token
+ *              included). With causal != 0, query qi sees ctx_lens[b] - (Q-1-qi)
+ *              keys; otherwise every query sees ctx_lens[b].
+ *   max_ctx  : upper bound of ctx_lens (sizes the launch grid).
+ * A row with 0 visible keys gets a zero output.
+ * Reference: models.py:126-165, :444-466; scripts/evaluate_paging_variants.py:56-133.
+ */
+SKV_API int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
+                        const void* k_pool, const void* v_pool,
+                        const int32_t* block_tables, int32_t table_stride,
+                        const int32_t* table_rows,
+                        const int32_t* ctx_lens,
+                        void* out, int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h,
+                        int32_t batch, int32_t q_len, int32_t num_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                        int32_t max_ctx, float scale, int32_t causal, int32_t dtype,
+                        int32_t chunk_tokens, void* partials, int64_t partial_bytes,
+                        int32_t* counters, int64_t counter_count, void* stream);
+
+/*
+ * skv_dense_attention — attention over contiguous K/V.
+ *   K/V element (slot s, kv head h, position t, dim d) is at
+ *   k[s*kv_stride_s + h*kv_stride_h + t*kv_stride_t + d] (same strides for v).
+ *   Row b reads slot slot_ids ? slot_ids[b] : b.
+ *   lens  : int32 [B] keys visible to the last query of row b (causal as above).
+ * Used for cross-attention over g_cross_kv [S, L, 2, H, T_enc, D] slices and for
+ * causal attention over contiguous prompt K/V.
+ * Reference: models.py:167-203, :468-479, :126-165 (contiguous past).
+ */
+SKV_API int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
+                        const void* k, const void* v,
+                        int64_t kv_stride_s, int64_t kv_stride_h, int64_t kv_stride_t,
+                        const int32_t* slot_ids,
+                        const int32_t* lens,
+                        void* out, int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h,
+                        int32_t batch, int32_t q_len, int32_t num_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t max_len, float scale, int32_t causal,
+                        int32_t dtype, int32_t chunk_tokens,
+                        void* partials, int64_t partial_bytes,
+                        int32_t* counters, int64_t counter_count, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPEECH_KV_H_ */

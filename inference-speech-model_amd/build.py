@@ -1,0 +1,72 @@
+"""Build libspeechkv.so (gfx950 HIP kernels + C ABI) in-tree with hipcc.
+
+Usage:  python inference-speech-model_amd/build.py [--debug]
+
+The library lands next to the Python package that loads it
+(speech_serving/libspeechkv.so) so it travels with the source tree.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_ROOT = os.path.dirname(os.path.abspath(__file__))
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+CSRC = os.path.join(PKG_ROOT, "csrc")
+INCLUDE = os.path.join(REPO_ROOT, "include")
+SOURCES = [os.path.join(CSRC, "skv_kernels.hip")]
+OUTPUT = os.path.join(PKG_ROOT, "speech_serving", "libspeechkv.so")
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def build(debug: bool = False, verbose: bool = False) -> str:
+    """Compile every HIP source into one shared library; returns its path."""
+    tmp = OUTPUT + ".tmp"
+    cmd = [
+        hipcc(),
+        f"--offload-arch={ARCH}",
+        "-std=c++17",
+        "-O1" if debug else "-O3",
+        "-fPIC",
+        "-shared",
+        # Packed fp32 VALU ops are kept out of every kernel on purpose.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-fvisibility=hidden",
+        "-I", INCLUDE,
+        "-I", CSRC,
+        "-Wno-unused-parameter",
+        "-o", tmp,
+        *SOURCES,
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, OUTPUT)
+    return OUTPUT
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--debug", action="store_true")
+    ap.add_argument("-v", "--verbose", action="store_true")
+    args = ap.parse_args()
+    print(build(debug=args.debug, verbose=args.verbose))
+
+
+if __name__ == "__main__":
+    main()

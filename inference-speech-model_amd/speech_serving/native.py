@@ -1,0 +1,365 @@
+"""ctypes binding of libspeechkv.so — the gfx950 decoder KV-cache kernels.
+
+Every function here launches a hand-written HIP kernel on the caller's current
+stream. There is no fallback: a missing library or a tensor that is not on a
+GPU raises RuntimeError.
+
+Functions:
+    append(k_new, v_new, k_pool, v_pool, slot_mapping)
+    gather(k_pool, v_pool, block_tables, lens, max_len)
+    paged_attention(q, k_pool, v_pool, block_tables, ctx_lens, max_ctx, scale, ...)
+    dense_attention(q, k, v, lens, max_len, scale, ...)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Dict, Optional, Tuple
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libspeechkv.so")
+_lib: Optional[ctypes.CDLL] = None
+_lib_lock = threading.Lock()
+
+SKV_F32, SKV_F16, SKV_BF16 = 0, 1, 2
+_DTYPE_CODE = {torch.float32: SKV_F32, torch.float16: SKV_F16, torch.bfloat16: SKV_BF16}
+
+# Exported entry points and their ctypes signatures (must match include/speech_kv.h).
+_c_int, _c_i32, _c_i64, _c_p, _c_f = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
+SIGNATURES = {
+    "skv_version": (ctypes.c_char_p, []),
+    "skv_last_error": (ctypes.c_char_p, []),
+    "skv_append": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_p]),
+    "skv_gather": (_c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                            _c_i32, _c_i32, _c_p]),
+    "skv_attention_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "skv_default_chunk_tokens": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "skv_paged_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p,
+                                     _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                     _c_i32, _c_i32, _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_i64,
+                                     _c_p]),
+    "skv_dense_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p,
+                                     _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                     _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_p]),
+}
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """Load libspeechkv.so (after torch, so it binds to torch's HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is None:
+            if not os.path.exists(_LIB_PATH):
+                raise RuntimeError(
+                    f"libspeechkv.so not found at {_LIB_PATH}; build it with "
+                    "`python inference-speech-model_amd/build.py`")
+            handle = ctypes.CDLL(_LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = handle
+    return _lib
+
+
+def version() -> str:
+    return lib().skv_version().decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().skv_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def _code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16") from None
+
+
+def _gpu(t: torch.Tensor, name: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a GPU tensor (got device {t.device}); the HIP kernels have no CPU path")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
+    _gpu(t, name)
+    if t.dtype != torch.int32:
+        raise RuntimeError(f"{name} must be int32 (got {t.dtype})")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    return t
+
+
+# ---------------------------------------------------------------------------
+# Split-K scratch, one pair per device: `partials` (any content) and
+# `counters` (int32, zero-filled once, used for arrival counters only; every
+# attention launch leaves them zero). Both grow only outside graph capture.
+# ---------------------------------------------------------------------------
+_partials: Dict[int, torch.Tensor] = {}
+_counters: Dict[int, torch.Tensor] = {}
+
+
+def _dev_index(device) -> int:
+    idx = torch.device(device).index
+    return torch.cuda.current_device() if idx is None else idx
+
+
+def reserve_workspace(partial_bytes: int, counter_count: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Return (partials uint8, counters int32) of at least the requested sizes."""
+    idx = _dev_index(device)
+    part = _partials.get(idx)
+    cnt = _counters.get(idx)
+    grow_p = part is None or part.numel() < partial_bytes
+    grow_c = cnt is None or cnt.numel() < counter_count
+    if grow_p or grow_c:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"attention scratch ({partial_bytes} B partials, {counter_count} counters) must be reserved "
+                "before graph capture")
+        dev = torch.device("cuda", idx)
+        if grow_p:
+            size = max(int(partial_bytes), 1 << 20, 0 if part is None else 2 * part.numel())
+            part = torch.empty(size, dtype=torch.uint8, device=dev)
+            _partials[idx] = part
+        if grow_c:
+            size = max(int(counter_count), 4096, 0 if cnt is None else 2 * cnt.numel())
+            cnt = torch.zeros(size, dtype=torch.int32, device=dev)
+            _counters[idx] = cnt
+    return part, cnt
+
+
+def reserve_attention(rows: int, heads: int, head_dim: int, max_len: int, dtype: torch.dtype, device,
+                      chunk_tokens: int = 0) -> None:
+    """Pre-size the scratch for an attention call shape (call before graph capture)."""
+    need = attention_workspace_bytes(rows, heads, head_dim, max(max_len, 1), dtype, chunk_tokens)
+    if need > 0:
+        reserve_workspace(need, rows * heads, device)
+
+
+def _scratch(rows: int, heads: int, need: int, device):
+    if need <= 0:
+        return None, 0, None, 0
+    part, cnt = reserve_workspace(need, rows * heads, device)
+    return part.data_ptr(), part.numel(), cnt.data_ptr(), cnt.numel()
+
+
+def attention_workspace_bytes(rows: int, heads: int, head_dim: int, max_len: int, dtype: torch.dtype,
+                              chunk_tokens: int = 0) -> int:
+    return int(lib().skv_attention_workspace_bytes(rows, heads, head_dim, max_len, chunk_tokens, _code(dtype)))
+
+
+def default_chunk_tokens(rows: int, heads: int, head_dim: int, max_len: int, dtype: torch.dtype) -> int:
+    return int(lib().skv_default_chunk_tokens(rows, heads, head_dim, max_len, _code(dtype)))
+
+
+# ---------------------------------------------------------------------------
+# Entry points.
+# ---------------------------------------------------------------------------
+def append(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_pool: torch.Tensor,
+           v_pool: Optional[torch.Tensor], slot_mapping: torch.Tensor) -> None:
+    """pool[slot // BS, slot % BS] = new row, for each of the N rows of k_new/v_new.
+
+    k_new, v_new: [N, H, D] (any row/head strides, D contiguous).
+    k_pool, v_pool: [num_blocks, block_size, H, D] contiguous.
+    slot_mapping: int64 [N]; a negative slot skips the row.
+    Same bytes as `key_pool[l][blk, off] = new_k` in the reference
+    (speech_serving/phase_aware_scheduler.py:1004-1010).
+    """
+    for t, n in ((k_new, "k_new"), (k_pool, "k_pool"), (slot_mapping, "slot_mapping")):
+        _gpu(t, n)
+    if (v_new is None) != (v_pool is None):
+        raise RuntimeError("append: v_new and v_pool must both be given or both be None")
+    if k_new.dim() != 3:
+        raise RuntimeError(f"append: k_new must be [N, H, D], got {tuple(k_new.shape)}")
+    n, h, d = k_new.shape
+    if k_pool.dim() != 4 or k_pool.shape[2] != h or k_pool.shape[3] != d or not k_pool.is_contiguous():
+        raise RuntimeError(f"append: pool {tuple(k_pool.shape)} does not match rows [*, *, {h}, {d}] / not contiguous")
+    if k_new.dtype != k_pool.dtype:
+        k_new = k_new.to(k_pool.dtype)
+    if k_new.stride(2) != 1:
+        k_new = k_new.contiguous()
+    if v_new is not None:
+        _gpu(v_new, "v_new")
+        _gpu(v_pool, "v_pool")
+        if v_pool.shape != k_pool.shape or v_pool.dtype != k_pool.dtype or not v_pool.is_contiguous():
+            raise RuntimeError("append: v_pool must match k_pool")
+        if v_new.dtype != v_pool.dtype:
+            v_new = v_new.to(v_pool.dtype)
+        if v_new.shape != k_new.shape:
+            raise RuntimeError("append: v_new must match k_new's shape")
+        if v_new.stride() != k_new.stride():
+            k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != n:
+        raise RuntimeError(f"append: slot_mapping must be int64 [{n}]")
+    slot_mapping = slot_mapping.contiguous()
+    num_slots = k_pool.shape[0] * k_pool.shape[1]
+    rc = lib().skv_append(k_new.data_ptr(), _ptr(v_new), k_new.stride(0), k_new.stride(1), k_pool.data_ptr(),
+                          _ptr(v_pool), slot_mapping.data_ptr(), n, h, d, num_slots, _code(k_pool.dtype),
+                          _stream(k_pool.device))
+    _check(rc, "skv_append")
+
+
+def gather(k_pool: torch.Tensor, v_pool: Optional[torch.Tensor], block_tables: torch.Tensor,
+           lens: torch.Tensor, max_len: int, k_out: Optional[torch.Tensor] = None,
+           v_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Contiguous [B, H, max_len, D] copies of the paged K/V, zero beyond lens[b].
+
+    Row b's token t comes from pool[block_tables[b, t // BS], t % BS]; this is
+    `pool[table].view(-1, H, D)[:T].permute(1, 0, 2)` of the reference
+    (speech_serving/tts_engine.py:177-185) batched with zero padding
+    (speech_serving/phase_aware_scheduler.py:818-830).
+    """
+    _gpu(k_pool, "k_pool")
+    block_tables = _i32(block_tables, "block_tables")
+    lens = _i32(lens, "lens")
+    if block_tables.dim() != 2:
+        raise RuntimeError("gather: block_tables must be [B, max_blocks]")
+    b = block_tables.shape[0]
+    nb, bs, h, d = k_pool.shape
+    if not k_pool.is_contiguous():
+        raise RuntimeError("gather: pool must be contiguous")
+    if lens.numel() < b:
+        raise RuntimeError(f"gather: lens has {lens.numel()} entries for {b} rows")
+    if k_out is None:
+        k_out = torch.empty((b, h, max_len, d), dtype=k_pool.dtype, device=k_pool.device)
+    if v_pool is not None and v_out is None:
+        v_out = torch.empty((b, h, max_len, d), dtype=v_pool.dtype, device=v_pool.device)
+    for t in (k_out, v_out):
+        if t is not None and (tuple(t.shape) != (b, h, max_len, d) or not t.is_contiguous()):
+            raise RuntimeError(f"gather: output must be contiguous [{b}, {h}, {max_len}, {d}]")
+    if v_pool is not None and (v_pool.shape != k_pool.shape or not v_pool.is_contiguous()):
+        raise RuntimeError("gather: v_pool must match k_pool")
+    rc = lib().skv_gather(k_pool.data_ptr(), _ptr(v_pool), block_tables.data_ptr(), block_tables.shape[1],
+                          lens.data_ptr(), k_out.data_ptr(), _ptr(v_out), b, h, d, bs, nb, max_len,
+                          _code(k_pool.dtype), _stream(k_pool.device))
+    _check(rc, "skv_gather")
+    return k_out, v_out
+
+
+def _q4(q: torch.Tensor, name: str) -> torch.Tensor:
+    """View q/out as [B, Q, H, D]; a 3-D input is [B, H, D] with Q = 1."""
+    if q.dim() == 3:
+        return q.unsqueeze(1)
+    if q.dim() == 4:
+        return q
+    raise RuntimeError(f"{name} must be [B, H, D] or [B, Q, H, D], got {tuple(q.shape)}")
+
+
+def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
+                    ctx_lens: torch.Tensor, max_ctx: int, scale: float, causal: bool = False,
+                    table_rows: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                    chunk_tokens: int = 0) -> torch.Tensor:
+    """softmax(q K^T * scale) V over each row's paged K/V.
+
+    q: [B, H, D] or [B, Q, H, D]; pools [num_blocks, BS, Hkv, D]; block_tables
+    int32 [*, max_blocks]; ctx_lens int32 [B] = keys visible to the last query
+    (new token included); causal: query qi sees ctx_lens[b] - (Q - 1 - qi) keys.
+    Reference math: speech_serving/models.py:126-165 and :444-466.
+    """
+    for t, n in ((q, "q"), (k_pool, "k_pool"), (v_pool, "v_pool")):
+        _gpu(t, n)
+    block_tables = _i32(block_tables, "block_tables")
+    ctx_lens = _i32(ctx_lens, "ctx_lens")
+    if table_rows is not None:
+        table_rows = _i32(table_rows, "table_rows")
+    q4 = _q4(q, "q")
+    bsz, qlen, heads, d = q4.shape
+    nb, bs, hkv, dk = k_pool.shape
+    if dk != d or v_pool.shape != k_pool.shape or not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise RuntimeError("paged_attention: pools must be contiguous [num_blocks, BS, Hkv, D] matching q")
+    if q4.dtype != k_pool.dtype or v_pool.dtype != k_pool.dtype:
+        raise RuntimeError(f"paged_attention: dtype mismatch q={q4.dtype} pool={k_pool.dtype}")
+    if block_tables.dim() != 2 or ctx_lens.numel() < bsz:
+        raise RuntimeError("paged_attention: block_tables must be 2-D and ctx_lens must cover the batch")
+    if table_rows is None and block_tables.shape[0] < bsz:
+        raise RuntimeError(f"paged_attention: {block_tables.shape[0]} table rows for batch {bsz}")
+    if table_rows is not None and table_rows.numel() < bsz:
+        raise RuntimeError("paged_attention: table_rows must cover the batch")
+    if q4.stride(3) != 1:
+        q4 = q4.contiguous()
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    o4 = _q4(out, "out")
+    if tuple(o4.shape) != tuple(q4.shape) or o4.stride(3) != 1:
+        raise RuntimeError("paged_attention: out must match q's shape with contiguous head_dim")
+    code = _code(q4.dtype)
+    max_ctx = max(0, min(int(max_ctx), block_tables.shape[1] * bs))
+    if chunk_tokens <= 0:
+        chunk_tokens = default_chunk_tokens(bsz * qlen, heads, d, max(max_ctx, 1), q4.dtype)
+    need = attention_workspace_bytes(bsz * qlen, heads, d, max_ctx, q4.dtype, chunk_tokens)
+    pp, pn, cp, cn = _scratch(bsz * qlen, heads, need, q.device)
+    rc = lib().skv_paged_attention(
+        q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2), k_pool.data_ptr(), v_pool.data_ptr(),
+        block_tables.data_ptr(), block_tables.stride(0), _ptr(table_rows), ctx_lens.data_ptr(),
+        o4.data_ptr(), o4.stride(0), o4.stride(1), o4.stride(2), bsz, qlen, heads, hkv, d, bs, nb, max_ctx,
+        float(scale), 1 if causal else 0, code, chunk_tokens, pp, pn, cp, cn, _stream(q.device))
+    _check(rc, "skv_paged_attention")
+    return out
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: torch.Tensor, max_len: int,
+                    scale: float, causal: bool = False, slot_ids: Optional[torch.Tensor] = None,
+                    out: Optional[torch.Tensor] = None, chunk_tokens: int = 0) -> torch.Tensor:
+    """Attention over contiguous K/V laid out [S, Hkv, T, D] (any strides, D contiguous).
+
+    Row b attends slot slot_ids[b] (or b) over its first lens[b] positions.
+    Cross-attention reference: speech_serving/models.py:167-203 and :468-479.
+    """
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _gpu(t, n)
+    lens = _i32(lens, "lens")
+    if slot_ids is not None:
+        slot_ids = _i32(slot_ids, "slot_ids")
+    if k.dim() != 4 or v.shape != k.shape or k.stride() != v.stride() or k.stride(3) != 1:
+        raise RuntimeError("dense_attention: k/v must be [S, Hkv, T, D] with equal strides, D contiguous")
+    q4 = _q4(q, "q")
+    bsz, qlen, heads, d = q4.shape
+    _, hkv, tmax, dk = k.shape
+    if dk != d:
+        raise RuntimeError("dense_attention: head_dim mismatch")
+    if lens.numel() < bsz:
+        raise RuntimeError("dense_attention: lens must cover the batch")
+    if slot_ids is None and k.shape[0] < bsz:
+        raise RuntimeError(f"dense_attention: {k.shape[0]} K/V slots for batch {bsz}")
+    if slot_ids is not None and slot_ids.numel() < bsz:
+        raise RuntimeError("dense_attention: slot_ids must cover the batch")
+    if q4.dtype != k.dtype or v.dtype != k.dtype:
+        raise RuntimeError(f"dense_attention: dtype mismatch q={q4.dtype} k={k.dtype}")
+    if q4.stride(3) != 1:
+        q4 = q4.contiguous()
+    if out is None:
+        out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    o4 = _q4(out, "out")
+    if tuple(o4.shape) != tuple(q4.shape) or o4.stride(3) != 1:
+        raise RuntimeError("dense_attention: out must match q's shape with contiguous head_dim")
+    max_len = max(0, min(int(max_len), tmax))
+    if chunk_tokens <= 0:
+        chunk_tokens = default_chunk_tokens(bsz * qlen, heads, d, max(max_len, 1), q4.dtype)
+    need = attention_workspace_bytes(bsz * qlen, heads, d, max_len, q4.dtype, chunk_tokens)
+    pp, pn, cp, cn = _scratch(bsz * qlen, heads, need, q.device)
+    rc = lib().skv_dense_attention(
+        q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2), k.data_ptr(), v.data_ptr(),
+        k.stride(0), k.stride(1), k.stride(2), _ptr(slot_ids), lens.data_ptr(), o4.data_ptr(),
+        o4.stride(0), o4.stride(1), o4.stride(2), bsz, qlen, heads, hkv, d, max_len, float(scale),
+        1 if causal else 0, _code(q4.dtype), chunk_tokens, pp, pn, cp, cn, _stream(q.device))
+    _check(rc, "skv_dense_attention")
+    return out

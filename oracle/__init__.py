@@ -1,0 +1,19 @@
+"""CPU oracle for the decoder KV-cache hot path — TEST INFRASTRUCTURE ONLY.
+
+A plain numpy restatement of the reference engine's arithmetic on this path,
+written from the reference's source text (file:line cited per function):
+
+    oracle.paged_kv   slot mapping, paged append, block-table gather, softmax
+                      attention (length-masked and padded/masked forms), paged
+                      attention = gather + attention.
+    oracle.decoder    the synthetic Whisper-class decoder (DecoderLayer.forward,
+                      decode_step, greedy decoding) used for token parity.
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import
+anything from this package, and only as the checker (or, in bench.py, as the
+timed CPU baseline). The product path (speech_serving) never imports it.
+
+Pinning: every oracle function is checked in tests/test_oracle.py against
+closed forms, invariants, brute force on tiny inputs and (for the decoder)
+golden vectors in tests/golden/. See each test for which function it pins.
+"""

@@ -1,0 +1,38 @@
+"""Shared pytest setup: import paths and the `gpu` marker.
+
+GPU tests run on a machine with a HIP device. Where no GPU exists at all
+(no /dev/kfd) they are skipped; on a machine that has /dev/kfd but where torch
+cannot see the GPU they fail, so a broken GPU setup is never a silent pass.
+"""
+import os
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "inference-speech-model_amd")
+for p in (PKG, ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import pytest  # noqa: E402
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a HIP GPU (MI355X)")
+
+
+def pytest_collection_modifyitems(config, items):
+    if os.path.exists("/dev/kfd"):
+        return
+    skip = pytest.mark.skip(reason="no GPU on this machine (/dev/kfd absent)")
+    for item in items:
+        if "gpu" in item.keywords:
+            item.add_marker(skip)
+
+
+@pytest.fixture(scope="session")
+def cuda():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test on a machine with /dev/kfd but torch.cuda.is_available() is False")
+    return torch.device("cuda", 0)

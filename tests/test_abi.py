@@ -1,0 +1,116 @@
+"""The C-ABI library loads, exports every symbol the header declares, and
+rejects bad arguments before launching anything (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from speech_serving import native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "speech_kv.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return set(re.findall(r"SKV_API\s+[\w\s\*]+?\b(skv_\w+)\s*\(", text))
+
+
+def test_header_declares_the_bound_entry_points():
+    decl = declared_symbols()
+    assert decl == set(native.SIGNATURES), (decl, set(native.SIGNATURES))
+    assert {"skv_append", "skv_gather", "skv_paged_attention", "skv_dense_attention"} <= decl
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = native.lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert "gfx950" in native.version()
+
+
+def test_no_undeclared_exports():
+    # The .so exports exactly the header's entry points (hidden visibility elsewhere).
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", native.library_path()], capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr
+    exported = {ln.split()[-1] for ln in out.stdout.splitlines() if " T " in ln}
+    assert exported == declared_symbols(), exported ^ declared_symbols()
+
+
+def test_workspace_bytes_formula():
+    lib = native.lib()
+    # 64 rows x 32 heads, keys up to 448 in chunks of 64 -> 7 chunks of (64 + 4) floats each.
+    got = lib.skv_attention_workspace_bytes(64, 32, 64, 448, 64, native.SKV_F16)
+    assert got == 64 * 32 * 7 * (64 + 4) * 4
+    # one chunk covers every key: no workspace
+    assert lib.skv_attention_workspace_bytes(64, 32, 64, 448, 512, native.SKV_F16) == 0
+    assert lib.skv_attention_workspace_bytes(0, 32, 64, 448, 64, native.SKV_F16) == 0
+
+
+def test_default_chunk():
+    lib = native.lib()
+    # fp16 D=64: 8 rows per wave instruction x 8 unrolled = 64-key sub-chunk
+    assert lib.skv_default_chunk_tokens(64, 32, 64, 448, native.SKV_F16) == 64
+    # many long rows: chunk grows until <= 16K waves
+    c = lib.skv_default_chunk_tokens(64, 20, 64, 1500, native.SKV_BF16)
+    assert c % 64 == 0 and 64 * 20 * -(-1500 // c) <= 16384
+    # fp32 D=64: 4 rows per instruction x 8 = 32
+    assert lib.skv_default_chunk_tokens(1, 1, 64, 10, native.SKV_F32) == 32
+
+
+FAKE = 1 << 20  # aligned, never dereferenced: validation fails before any launch
+
+
+def test_append_rejects_bad_dtype():
+    lib = native.lib()
+    rc = lib.skv_append(FAKE, FAKE, 64, 64, FAKE, FAKE, FAKE, 4, 1, 64, 16, 7, None)
+    assert rc == -2 and b"dtype" in lib.skv_last_error()
+
+
+def test_append_rejects_misaligned_stride():
+    lib = native.lib()
+    rc = lib.skv_append(FAKE, FAKE, 63, 64, FAKE, FAKE, FAKE, 4, 1, 64, 16, native.SKV_F16, None)
+    assert rc == -3
+
+
+def test_attention_rejects_unsupported_head_dim():
+    lib = native.lib()
+    rc = lib.skv_paged_attention(FAKE, 48, 48, 48, FAKE, FAKE, FAKE, 4, None, FAKE, FAKE, 48, 48, 48,
+                                 1, 1, 1, 1, 48, 16, 8, 64, 1.0, 0, native.SKV_F16, 0, None, 0, None, 0, None)
+    assert rc == -1 and b"head_dim" in lib.skv_last_error()
+
+
+def test_attention_requires_workspace_for_split_keys():
+    lib = native.lib()
+    rc = lib.skv_dense_attention(FAKE, 64, 64, 64, FAKE, FAKE, 64 * 1500, 64 * 1500, 64, None, FAKE, FAKE,
+                                 64, 64, 64, 4, 1, 1, 1, 64, 1500, 0.125, 0, native.SKV_F16, 64, None, 0, None, 0,
+                                 None)
+    assert rc == -4 and b"partials" in lib.skv_last_error()
+    # partials present but counters missing
+    rc = lib.skv_dense_attention(FAKE, 64, 64, 64, FAKE, FAKE, 64 * 1500, 64 * 1500, 64, None, FAKE, FAKE,
+                                 64, 64, 64, 4, 1, 1, 1, 64, 1500, 0.125, 0, native.SKV_F16, 64, FAKE, 1 << 30, None,
+                                 0, None)
+    assert rc == -4 and b"counters" in lib.skv_last_error()
+
+
+def test_attention_rejects_bad_group():
+    lib = native.lib()
+    rc = lib.skv_dense_attention(FAKE, 64, 64, 64, FAKE, FAKE, 64, 64, 64, None, FAKE, FAKE, 64, 64, 64,
+                                 1, 1, 3, 2, 64, 10, 0.125, 0, native.SKV_F16, 0, None, 0, None, 0, None)
+    assert rc == -1
+
+
+def test_python_wrapper_refuses_cpu_tensors():
+    import torch
+
+    q = torch.zeros(1, 1, 64, dtype=torch.float16)
+    pool = torch.zeros(4, 16, 1, 64, dtype=torch.float16)
+    tbl = torch.zeros(1, 1, dtype=torch.int32)
+    lens = torch.ones(1, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        native.paged_attention(q, pool, pool, tbl, lens, 1, 0.125)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        native.append(q, q, pool, pool, torch.zeros(1, dtype=torch.int64))
