@@ -1,0 +1,306 @@
+"""Benchmark of the decoder KV-cache hot path on one MI355X.
+
+Workload (default): paged decode attention for one decoder layer, fp16,
+32 heads x 64, block size 16, batch 64, per-sequence context U[1, 448], block
+tables a seeded random permutation of a 4096-block pool, Q/K/V ~ N(0, 1).
+One step = one fused launch that appends the batch's new token K/V into the
+pool through each sequence's block table and attends over the sequence's
+context (new token included). Inputs are resident in HBM before timing. Steps rotate over
+independent pool/table sets whose combined footprint exceeds the 256 MB
+last-level cache, so every step streams its K/V from HBM.
+
+Prints one JSON line: value = whole-step algorithmic HBM throughput (GB/s);
+`roofline` = the attention kernel alone (HIP events around each launch on
+its stream); `cpu_baseline` = the numpy oracle on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "inference-speech-model_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak
+LLC_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--heads", type=int, default=32)
+    ap.add_argument("--head-dim", type=int, default=64)
+    ap.add_argument("--block-size", type=int, default=16)
+    ap.add_argument("--pool-blocks", type=int, default=4096)
+    ap.add_argument("--max-ctx", type=int, default=448)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--chunk", type=int, default=0, help="split-K chunk (0 = library default)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--mode", choices=["attention", "copy"], default="attention",
+                    help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling")
+    ap.add_argument("--copy-mib", type=int, default=512)
+    return ap.parse_args()
+
+
+def copy_calibration(a):
+    """Copy a buffer of known size --steps times (reads and writes copy-mib MiB each)."""
+    import torch
+
+    n = a.copy_mib << 20
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / a.steps
+    print(json.dumps({"mode": "copy", "bytes_read_per_launch": n, "bytes_written_per_launch": n,
+                      "launches": a.steps + 3, "us_per_copy": round(dt * 1e6, 2),
+                      "GBps_read_plus_write": round(2 * n / dt / 1e9, 1)}), flush=True)
+
+
+def measured_traffic(a):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary of this exact config, else None."""
+    key = (f"fp16/b{a.batch}/h{a.heads}/d{a.head_dim}/bs{a.block_size}/nb{a.pool_blocks}/"
+           f"ctx{a.max_ctx}/seed{a.seed}")
+    path = os.path.join(ROOT, "profiles", "paged_attention_config2.md")
+    if a.chunk or not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch=") and line.split("config=")[-1].strip() == key:
+            return int(line.split()[0].split("=")[1])
+    return None
+
+
+def attention_bytes(ctx, heads, d, elt, bs):
+    """Algorithmic bytes of one paged attention launch: K+V rows read, q read,
+    out written, block-table entries and the length read."""
+    return sum(2 * c * heads * d * elt + 2 * heads * d * elt + 4 * math.ceil(c / bs) + 4 for c in ctx)
+
+
+def append_write_bytes(batch, heads, d, elt):
+    """Pool bytes the fused append writes (the new rows themselves are read as keys)."""
+    return batch * 2 * heads * d * elt
+
+
+def append_bytes(batch, heads, d, elt):
+    """Standalone append: read the new rows, write them, read the slot ids."""
+    return batch * (2 * heads * d * elt + 2 * heads * d * elt + 8)
+
+
+class ProblemSet:
+    """One independent copy of the workload: pool, tables, lengths, inputs."""
+
+    def __init__(self, torch, a, seed, device, dtype):
+        g = torch.Generator().manual_seed(seed)
+        b, h, d, bs, nb = a.batch, a.heads, a.head_dim, a.block_size, a.pool_blocks
+        self.ctx = torch.randint(1, a.max_ctx + 1, (b,), generator=g)  # keys incl. the new token
+        maxblk = math.ceil(a.max_ctx / bs)
+        perm = torch.randperm(nb, generator=g)[: b * maxblk]
+        self.tables_cpu = perm.view(b, maxblk).to(torch.int32)
+        self.k_pool = torch.randn(nb, bs, h, d, generator=g).to(device, dtype)
+        self.v_pool = torch.randn(nb, bs, h, d, generator=g).to(device, dtype)
+        self.q = torch.randn(b, h, d, generator=g).to(device, dtype)
+        self.k_new = torch.randn(b, h, d, generator=g).to(device, dtype)
+        self.v_new = torch.randn(b, h, d, generator=g).to(device, dtype)
+        pos = (self.ctx - 1).tolist()
+        slots = [int(self.tables_cpu[i, p // bs]) * bs + p % bs for i, p in enumerate(pos)]
+        self.slots = torch.tensor(slots, dtype=torch.int64, device=device)
+        self.tables = self.tables_cpu.to(device)
+        self.ctx_dev = self.ctx.to(torch.int32).to(device)
+        self.out = torch.empty_like(self.q)
+
+
+def cpu_baseline(sets, a, scale, budget_s):
+    """Time the numpy oracle (float64, one thread) on whole config batches."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import paged_kv as O
+
+    s = sets[0]
+    kp = s.k_pool.float().cpu().numpy()
+    vp = s.v_pool.float().cpu().numpy()
+    q = s.q.float().cpu().numpy()[:, None]
+    tables = s.tables_cpu.numpy()
+    ctx = s.ctx.tolist()
+    knew = s.k_new.float().cpu().numpy()
+    vnew = s.v_new.float().cpu().numpy()
+    slots = s.slots.cpu().tolist()
+    nbytes = attention_bytes(ctx, a.heads, a.head_dim, 2, a.block_size) + append_bytes(a.batch, a.heads,
+                                                                                      a.head_dim, 2)
+    passes = 0
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        while True:
+            O.append(kp, vp, knew, vnew, slots)
+            O.paged_attention(q, kp, vp, tables, ctx, scale)
+            passes += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+    per = el / passes
+    return {
+        "value": round(nbytes / per / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{passes} full batches (append + paged attention, B={a.batch}) by the numpy oracle, "
+                  f"{per * 1e3:.1f} ms per batch",
+        "ms_per_step": round(per * 1e3, 3),
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are not part of it",
+                          "n_gpus": a.gpus}))
+        sys.exit(2)
+    import torch
+
+    from speech_serving import native
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("bench.py needs a HIP GPU")
+    if a.mode == "copy":
+        copy_calibration(a)
+        return
+    dev = torch.device("cuda", 0)
+    dtype = torch.float16
+    elt = 2
+    scale = 1.0 / math.sqrt(a.head_dim)
+    native.lib()
+
+    # Enough independent sets that consecutive reuse exceeds the last-level cache twice over.
+    one = ProblemSet(torch, a, a.seed, dev, dtype)
+    touched = attention_bytes(one.ctx.tolist(), a.heads, a.head_dim, elt, a.block_size)
+    nsets = max(2, math.ceil(2 * LLC_BYTES / touched) + 1)
+    sets = [one] + [ProblemSet(torch, a, a.seed + i, dev, dtype) for i in range(1, nsets)]
+    native.reserve_attention(a.batch, a.heads, a.head_dim, a.max_ctx, dtype, dev, a.chunk)
+
+    def step(s):
+        native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, a.max_ctx, scale, out=s.out,
+                               chunk_tokens=a.chunk, k_new=s.k_new, v_new=s.v_new)
+
+    # One captured graph per set; a step replays the next set's graph.
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for s in sets:
+            step(s)
+    torch.cuda.current_stream().wait_stream(stream)
+    graphs = []
+    for s in sets:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(s)
+        graphs.append(g)
+    torch.cuda.synchronize()
+
+    for i in range(a.warmup):
+        graphs[i % nsets].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        graphs[i % nsets].replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / a.steps * 1e3
+
+    step_bytes = [attention_bytes(s.ctx.tolist(), a.heads, a.head_dim, elt, a.block_size) +
+                  append_write_bytes(a.batch, a.heads, a.head_dim, elt) for s in sets]
+    total_bytes = sum(step_bytes[i % nsets] for i in range(a.steps))
+    value = total_bytes / wall / 1e9
+
+    # Roofline of the dominant (and only) kernel: HIP events around each launch
+    # on the stream it runs on.
+    cur = torch.cuda.current_stream()
+    n_ev = max(60, 3 * nsets)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
+    attn_bytes = step_bytes
+    for i in range(n_ev):
+        s = sets[i % nsets]
+        evs[i][0].record(cur)
+        step(s)
+        evs[i][1].record(cur)
+    torch.cuda.synchronize()
+    durs_us = [evs[i][0].elapsed_time(evs[i][1]) * 1e3 for i in range(n_ev)]
+    skip = nsets  # first pass over the sets is warm-up
+    avg_us = sum(durs_us[skip:]) / (n_ev - skip)
+    avg_bytes = sum(attn_bytes[i % nsets] for i in range(skip, n_ev)) / (n_ev - skip)
+    achieved = avg_bytes / (avg_us * 1e-6) / 1e9
+
+    # Correctness guard on the measured data: one set against the oracle.
+    import numpy as np
+
+    from oracle import paged_kv as O
+
+    s = sets[0]
+    step(s)  # appends the same rows again: the pool is unchanged
+    torch.cuda.synchronize()
+    want = O.paged_attention(s.q.double().cpu().numpy()[:, None], s.k_pool.double().cpu().numpy(),
+                             s.v_pool.double().cpu().numpy(), s.tables_cpu.numpy(), s.ctx.tolist(), scale)[:, 0]
+    max_err = float(np.abs(s.out.double().cpu().numpy() - want).max())
+
+    result = {
+        "metric": "decode tokens/sec + paged-attn achieved HBM GB/s (% of peak), 1 GPU",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic N(0,1) q/k/v, seeded",
+        "config": {
+            "workload": "paged decode attention microbench: fused append + paged attention, fp16, "
+                        f"{a.heads} heads x {a.head_dim}, 1 layer, block size {a.block_size}, batch {a.batch}, "
+                        f"ctx U[1,{a.max_ctx}], {a.pool_blocks}-block pool with seeded permuted tables",
+            "batch": a.batch,
+            "heads": a.heads,
+            "head_dim": a.head_dim,
+            "block_size": a.block_size,
+            "pool_blocks": a.pool_blocks,
+            "max_ctx": a.max_ctx,
+            "rotating_sets": nsets,
+            "chunk_tokens": a.chunk or native.default_chunk_tokens(a.batch, a.heads, a.head_dim, a.max_ctx, dtype),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(a),
+            "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE per launch, scaled by a known-size copy (profiles/paged_attention_config2.md)",
+            "kernel": "attention_kernel<fp16, D=64, paged> with fused append",
+            "avg_launch_us": round(avg_us, 3),
+            "algorithmic_bytes_per_launch": int(avg_bytes),
+        },
+        "max_abs_err_vs_oracle": max_err,
+    }
+    if not a.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(sets, a, scale, a.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -67,7 +67,7 @@ enum skv_status {
   SKV_EINVAL = -1,     /* bad size / null pointer / unsupported head_dim */
   SKV_EDTYPE = -2,     /* unknown dtype code */
   SKV_EALIGN = -3,     /* pointer or stride not 16-byte aligned */
-  SKV_EWORKSPACE = -4  /* split-K partials or counters missing / too small */
+  SKV_EWORKSPACE = -4  /* workspace missing or smaller than skv_attention_workspace_bytes */
 };
 
 /* Library version string, e.g. "speechkv 0.1.0 gfx950". */
@@ -109,16 +109,12 @@ SKV_API int skv_gather(const void* k_pool, const void* v_pool,
                int32_t dtype, void* stream);
 
 /*
- * Split-K scratch for skv_paged_attention / skv_dense_attention. A call with
- * `rows` = batch * q_len query rows and `num_heads` heads whose keys span more
- * than one chunk of `chunk_tokens` (0 = library default for `dtype`) needs:
- *   partials : skv_attention_workspace_bytes(...) bytes, 16-byte aligned, any content;
- *   counters : int32 [rows * num_heads] arrival counters that are zero before
- *              the call; every call leaves them zero again. Keep the counter
- *              buffer for counters only (never reuse it as partials), so it
- *              stays zero between calls and across HIP-graph replays.
- * skv_attention_workspace_bytes returns 0 when every row fits one chunk (then
- * both pointers may be NULL).
+ * Workspace bytes needed by skv_paged_attention / skv_dense_attention for a
+ * call with `rows` = batch * q_len query rows and `num_heads` heads whose keys
+ * (up to `max_len`) are split into chunks of `chunk_tokens` (0 = library
+ * default for `dtype`). The workspace holds one (max, sum, acc[head_dim])
+ * fp32 partial per (row, head, chunk); any content is fine on entry. Returns 0
+ * when every row fits one chunk (then the workspace may be NULL).
  */
 SKV_API int64_t skv_attention_workspace_bytes(int32_t rows, int32_t num_heads, int32_t head_dim,
                                       int32_t max_len, int32_t chunk_tokens, int32_t dtype);
@@ -138,20 +134,28 @@ SKV_API int32_t skv_default_chunk_tokens(int32_t rows, int32_t num_heads, int32_
  *              included). With causal != 0, query qi sees ctx_lens[b] - (Q-1-qi)
  *              keys; otherwise every query sees ctx_lens[b].
  *   max_ctx  : upper bound of ctx_lens (sizes the launch grid).
+ *   k_new, v_new (optional, both or neither): [B, Q, num_kv_heads, D] rows of
+ *              the Q newest keys of each row, i.e. positions
+ *              ctx_lens[b]-Q .. ctx_lens[b]-1. The call appends them into the
+ *              pools at pool[table[pos / block_size], pos % block_size] (the
+ *              reference's slot-mapping scatter, phase_aware_scheduler.py:
+ *              1004-1010 and :681-690) and attends over them in the same launch.
  * A row with 0 visible keys gets a zero output.
  * Reference: models.py:126-165, :444-466; scripts/evaluate_paging_variants.py:56-133.
  */
 SKV_API int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
-                        const void* k_pool, const void* v_pool,
+                        void* k_pool, void* v_pool,
                         const int32_t* block_tables, int32_t table_stride,
                         const int32_t* table_rows,
                         const int32_t* ctx_lens,
+                        const void* k_new, const void* v_new,
+                        int64_t new_stride_b, int64_t new_stride_q, int64_t new_stride_h,
                         void* out, int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h,
                         int32_t batch, int32_t q_len, int32_t num_heads, int32_t num_kv_heads,
                         int32_t head_dim, int32_t block_size, int32_t num_blocks,
                         int32_t max_ctx, float scale, int32_t causal, int32_t dtype,
-                        int32_t chunk_tokens, void* partials, int64_t partial_bytes,
-                        int32_t* counters, int64_t counter_count, void* stream);
+                        int32_t chunk_tokens, void* workspace, int64_t workspace_bytes,
+                        void* stream);
 
 /*
  * skv_dense_attention — attention over contiguous K/V.
@@ -172,8 +176,7 @@ SKV_API int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_str
                         int32_t batch, int32_t q_len, int32_t num_heads, int32_t num_kv_heads,
                         int32_t head_dim, int32_t max_len, float scale, int32_t causal,
                         int32_t dtype, int32_t chunk_tokens,
-                        void* partials, int64_t partial_bytes,
-                        int32_t* counters, int64_t counter_count, void* stream);
+                        void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

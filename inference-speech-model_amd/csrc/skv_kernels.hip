@@ -2,19 +2,19 @@
 // speech serving engine: paged append, block-table gather, paged decode
 // attention and contiguous (cross-)attention. See speech_kv.h for the contract.
 //
-// Attention design (one launch, split-K with in-kernel merge):
-//   * One wave64 owns one (query row, head, key chunk). A 16-byte lane load
-//     carries EPL elements; LPT = D/EPL lanes cover one key row, so one wave
-//     instruction reads TPI = 64/LPT whole key rows (128 contiguous bytes each
-//     for fp16/bf16 at D=64) — fully coalesced per row.
-//   * Each lane group (TPI groups per wave) keeps its own base-2 online-softmax
-//     state over the keys it reads; the groups merge once at the end with lane
-//     exchanges. K and V for U key rows per group are loaded before any math,
-//     so a wave keeps U*2*16 B per lane (16 KB per wave at U=8) in flight.
-//   * Waves of the same (row, head) write (m, l, acc) partials to scratch and
-//     bump an arrival counter; the last arriving wave merges the partials,
-//     writes the output and resets the counter to zero (so the counter buffer
-//     needs zeroing once, and every launch is replay-safe inside a HIP graph).
+// Attention design:
+//   * One workgroup of kWaves wave64s owns one (query row, head, key chunk).
+//     For paged K/V the chunk's block ids are staged once into LDS, so the
+//     K/V loads of a wave never wait on a table load.
+//   * A 16-byte lane load carries EPL elements; LPT = D/EPL lanes cover one
+//     key row, so one wave instruction reads TPI = 64/LPT whole key rows
+//     (128 contiguous bytes each for fp16/bf16 at D=64). A wave loads K and V
+//     for U rows per lane group (a SUB = TPI*U-key sub-chunk) before any math.
+//   * Each lane group keeps its own base-2 online-softmax state; groups merge
+//     with lane exchanges, then the kWaves waves merge through LDS.
+//   * A row whose keys span several chunks writes one (m, l, acc) partial per
+//     chunk; merge_kernel (same stream, next launch) combines them. The kernel
+//     boundary orders the two, so no device-scope fence runs inside a kernel.
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
@@ -120,8 +120,15 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint4* __restrict__ k
 // ---------------------------------------------------------------------------
 // Attention.
 // ---------------------------------------------------------------------------
+#ifndef SKV_ATTN_WAVES
+#define SKV_ATTN_WAVES 4
+#endif
+constexpr int kWaves = SKV_ATTN_WAVES;  // waves per attention workgroup
+constexpr int kMaxChunkBlocks = 256;    // LDS block-id slots per chunk
+constexpr int kPartPad = 4;             // partial record = m, l, pad, pad, acc[D]
+
 struct AttnParams {
-  const uint4* q;   // element strides below are in 16-byte vector units
+  const uint4* q;  // strides below are in 16-byte vector units
   int64_t qsb, qsq, qsh;
   uint4* o;
   int64_t osb, osq, osh;
@@ -133,6 +140,11 @@ struct AttnParams {
   const int32_t* trows;
   int32_t bs, nb;
   int64_t row_vecs;  // vectors per pool token row = Hkv * D / EPL
+  // fused append (paged only): the Q newest keys of row b come from kn/vn
+  // [B, Q, Hkv, D] and are written into the pool through the row's table.
+  const uint4* kn;
+  const uint4* vn;
+  int64_t nsb, nsq, nsh;
   // contiguous addressing
   int64_t ss, sh, st;
   const int32_t* slots;
@@ -140,15 +152,20 @@ struct AttnParams {
   const int32_t* lens;
   int32_t batch, qlen, heads, group, max_len, causal, chunk, nchunk_max;
   float scale_log2;
-  float* part;      // [rows*heads*nchunk_max][D + 4]: m, l, -, -, acc[D]
-  int32_t* counts;  // [rows*heads]
+  float* part;  // [rows*heads*nchunk_max][D + kPartPad]
 };
-
-constexpr int kWavesPerBlock = 4;
 
 template <int TPI>
 constexpr int unroll_for() {
   return (64 / TPI) < 1 ? 1 : ((64 / TPI) > 8 ? 8 : (64 / TPI));
+}
+
+// Keys visible to query qi of batch row b.
+__device__ __forceinline__ int visible_len(const AttnParams& p, int b, int qi) {
+  int len = p.lens[b];
+  if (p.causal) len -= (p.qlen - 1 - qi);
+  len = len < 0 ? 0 : len;
+  return len > p.max_len ? p.max_len : len;
 }
 
 // Merge (m, l, acc) across the TPI lane groups of the wave (lane offsets
@@ -166,7 +183,7 @@ __device__ __forceinline__ void merge_groups(float& m, float& l, float* acc) {
   }
 }
 
-template <int DT, int D>
+template <int DT>
 __device__ __forceinline__ void write_out(const AttnParams& p, int64_t o_off, float l, const float* acc) {
   constexpr int EPL = Elt<DT>::EPL;
   const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -177,87 +194,124 @@ __device__ __forceinline__ void write_out(const AttnParams& p, int64_t o_off, fl
 }
 
 template <int DT, int D, bool PAGED>
-__global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
   constexpr int EPL = Elt<DT>::EPL;
   constexpr int LPT = D / EPL;
   constexpr int TPI = 64 / LPT;
   constexpr int U = unroll_for<TPI>();
-  constexpr int PSTRIDE = D + 4;
+  constexpr int SUB = TPI * U;
+  constexpr int PSTRIDE = D + kPartPad;
+
+  __shared__ int s_blk[PAGED ? kMaxChunkBlocks : 1];
+  __shared__ float s_ml[kWaves][2];
+  __shared__ float s_acc[kWaves][D];
 
   const int lane = threadIdx.x & 63;
-  const int64_t wid = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int wave = threadIdx.x >> 6;
   const int32_t rows = p.batch * p.qlen;
   const int64_t per_chunk = (int64_t)rows * p.heads;
-  const int chunk = (int)(wid / per_chunk);
+  const int chunk = (int)(blockIdx.x / per_chunk);
   if (chunk >= p.nchunk_max) return;
-  const int64_t rh = wid - (int64_t)chunk * per_chunk;  // row * heads + head
+  const int64_t rh = blockIdx.x - (int64_t)chunk * per_chunk;  // row * heads + head
   const int row = (int)(rh / p.heads);
   const int h = (int)(rh - (int64_t)row * p.heads);
   const int b = row / p.qlen;
   const int qi = row - b * p.qlen;
-
-  int len = p.lens[b];
-  if (p.causal) len -= (p.qlen - 1 - qi);
-  len = len < 0 ? 0 : len;
-  len = len > p.max_len ? p.max_len : len;
+  const int len = visible_len(p, b, qi);
   const int g = lane / LPT;
   const int j = lane - g * LPT;
   const int64_t o_off = (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh + j;
 
   if (len == 0) {
-    if (chunk == 0 && g == 0) p.o[o_off] = make_uint4(0u, 0u, 0u, 0u);
+    if (chunk == 0 && wave == 0 && g == 0) p.o[o_off] = make_uint4(0u, 0u, 0u, 0u);
     return;
   }
   const int nchunks = (len + p.chunk - 1) / p.chunk;
-  if (chunk >= nchunks) return;
-
-  const uint4 qv = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + j];
+  if (chunk >= nchunks) return;  // uniform over the workgroup
+  const int t_begin = chunk * p.chunk;
+  const int t_end = min(t_begin + p.chunk, len);
   const int kvh = h / p.group;
 
-  const int32_t* tbl = nullptr;
   int64_t base = 0;
+  int first_blk = 0;
+  int new_begin = 0x7fffffff;  // keys at positions >= new_begin come from kn/vn
+  int64_t nbase = 0;
   if constexpr (PAGED) {
     const int trow = p.trows ? p.trows[b] : b;
-    tbl = p.tables + (int64_t)trow * p.tstride;
+    const int32_t* tbl = p.tables + (int64_t)trow * p.tstride;
+    first_blk = t_begin / p.bs;
+    const int nblk = (t_end - 1) / p.bs - first_blk + 1;
+    for (int i = threadIdx.x; i < nblk; i += 64 * kWaves) {
+      const int blk = tbl[first_blk + i];
+      s_blk[i] = ((uint32_t)blk < (uint32_t)p.nb) ? blk : -1;
+    }
+    __syncthreads();
     base = (int64_t)kvh * LPT + j;
+    if (p.kn) {
+      new_begin = visible_len(p, b, p.qlen - 1) - p.qlen;
+      nbase = (int64_t)b * p.nsb - (int64_t)new_begin * p.nsq + (int64_t)kvh * p.nsh + j;
+      // Append: the last query row's workgroups of the first head of each KV
+      // group write the new keys of their chunk into the pool.
+      if (qi == p.qlen - 1 && h % p.group == 0) {
+        const int w0 = max(new_begin, t_begin);
+        const int nw = t_end - w0;
+        for (int i = threadIdx.x; i < 2 * nw * LPT; i += 64 * kWaves) {
+          const int kv = i >= nw * LPT;
+          const int r = i - kv * nw * LPT;
+          const int tt = w0 + r / LPT;
+          const int jj = r - (r / LPT) * LPT;
+          const int bi = tt / p.bs;
+          const int blk = s_blk[bi - first_blk];
+          if (blk >= 0) {
+            const int64_t dst = ((int64_t)blk * p.bs + (tt - bi * p.bs)) * p.row_vecs + (int64_t)kvh * LPT + jj;
+            const int64_t src = (int64_t)b * p.nsb + (int64_t)(tt - new_begin) * p.nsq + (int64_t)kvh * p.nsh + jj;
+            uint4* pool = const_cast<uint4*>(kv ? p.v : p.k);
+            pool[dst] = (kv ? p.vn : p.kn)[src];
+          }
+        }
+      }
+    }
   } else {
     const int slot = p.slots ? p.slots[b] : b;
     base = (int64_t)slot * p.ss + (int64_t)kvh * p.sh + j;
   }
+
+  const uint4 qv = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + j];
 
   float m = kNegInf, l = 0.f;
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
 
-  const int t_begin = chunk * p.chunk;
-  const int t_end = min(t_begin + p.chunk, len);
-  for (int s = t_begin; s < t_end; s += TPI * U) {
+  for (int s = t_begin + wave * SUB; s < t_end; s += kWaves * SUB) {
     uint4 kr[U], vr[U];
     bool ok[U];
+    const uint4* kp[U];
+    const uint4* vp[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t = s + u * TPI + g;
-      int64_t off = 0;
       bool valid = t < t_end;
       if constexpr (PAGED) {
-        if (valid) {
-          const int bi = t / p.bs;
-          const int blk = tbl[bi];
-          valid = (uint32_t)blk < (uint32_t)p.nb;
-          off = ((int64_t)blk * p.bs + (t - bi * p.bs)) * p.row_vecs + base;
-        }
+        const int bi = t / p.bs;
+        const int blk = valid ? s_blk[min(bi - first_blk, kMaxChunkBlocks - 1)] : -1;
+        valid = blk >= 0;
+        const int64_t off = ((int64_t)blk * p.bs + (t - bi * p.bs)) * p.row_vecs + base;
+        const int64_t noff = nbase + (int64_t)t * p.nsq;
+        const bool fresh = t >= new_begin;
+        kp[u] = fresh ? p.kn + noff : p.k + off;
+        vp[u] = fresh ? p.vn + noff : p.v + off;
       } else {
-        off = base + (int64_t)t * p.st;
+        const int64_t off = base + (int64_t)t * p.st;
+        kp[u] = p.k + off;
+        vp[u] = p.v + off;
       }
       ok[u] = valid;
-      if (valid) {
-        kr[u] = load_stream(p.k + off);
-        vr[u] = load_stream(p.v + off);
-      } else {
-        kr[u] = make_uint4(0u, 0u, 0u, 0u);
-        vr[u] = make_uint4(0u, 0u, 0u, 0u);
-      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      kr[u] = ok[u] ? load_stream(kp[u]) : make_uint4(0u, 0u, 0u, 0u);
+      vr[u] = ok[u] ? load_stream(vp[u]) : make_uint4(0u, 0u, 0u, 0u);
     }
     float sc[U];
     float mx = m;
@@ -283,37 +337,66 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
 
   merge_groups<LPT, EPL>(m, l, acc);
 
+  // Merge the kWaves wave states through LDS.
+  if (g == 0) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) s_acc[wave][j * EPL + e] = acc[e];
+    if (j == 0) {
+      s_ml[wave][0] = m;
+      s_ml[wave][1] = l;
+    }
+  }
+  __syncthreads();
+  if (wave != 0 || g != 0) return;
+  float M = s_ml[0][0], L = s_ml[0][1];
+  float A[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) A[e] = s_acc[0][j * EPL + e];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) merge_state<EPL>(M, L, A, s_ml[w][0], s_ml[w][1], &s_acc[w][j * EPL]);
+
   if (nchunks == 1) {
-    if (g == 0) write_out<DT, D>(p, o_off, l, acc);
+    write_out<DT>(p, o_off, L, A);
     return;
   }
-
-  // Split-K: publish this chunk's partial state, count arrivals.
-  float* part = p.part + rh * (int64_t)p.nchunk_max * PSTRIDE;
-  if (g == 0) {
-    float4* dst = reinterpret_cast<float4*>(part + (int64_t)chunk * PSTRIDE + 4 + j * EPL);
+  float* rec = p.part + (rh * p.nchunk_max + chunk) * PSTRIDE;
+  float4* dst = reinterpret_cast<float4*>(rec + kPartPad + j * EPL);
 #pragma unroll
-    for (int e = 0; e < EPL; e += 4) dst[e / 4] = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
-    if (j == 0) *reinterpret_cast<float2*>(part + (int64_t)chunk * PSTRIDE) = make_float2(m, l);
-  }
-  __threadfence();
-  int ticket = 0;
-  if (lane == 0) ticket = __hip_atomic_fetch_add(p.counts + rh, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-  ticket = __shfl(ticket, 0, 64);
-  if (ticket != nchunks - 1) return;
-  __threadfence();
-  if (lane == 0) __hip_atomic_store(p.counts + rh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int e = 0; e < EPL; e += 4) dst[e / 4] = make_float4(A[e], A[e + 1], A[e + 2], A[e + 3]);
+  if (j == 0) *reinterpret_cast<float2*>(rec) = make_float2(M, L);
+}
 
-  // Last arrival: merge all chunk partials (lane group g takes chunks g, g+TPI, ...).
+// Combine the per-chunk partials of rows that span more than one chunk.
+// One wave per (row, head); lane group g folds chunks g, g + TPI, ...
+template <int DT, int D>
+__global__ __launch_bounds__(256) void merge_kernel(AttnParams p) {
+  constexpr int EPL = Elt<DT>::EPL;
+  constexpr int LPT = D / EPL;
+  constexpr int TPI = 64 / LPT;
+  constexpr int PSTRIDE = D + kPartPad;
+  const int lane = threadIdx.x & 63;
+  const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int32_t rows = p.batch * p.qlen;
+  if (rh >= (int64_t)rows * p.heads) return;
+  const int row = (int)(rh / p.heads);
+  const int h = (int)(rh - (int64_t)row * p.heads);
+  const int b = row / p.qlen;
+  const int qi = row - b * p.qlen;
+  const int len = visible_len(p, b, qi);
+  const int nchunks = (len + p.chunk - 1) / p.chunk;
+  if (nchunks <= 1) return;
+  const int g = lane / LPT;
+  const int j = lane - g * LPT;
   float M = kNegInf, L = 0.f;
   float A[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) A[e] = 0.f;
+  const float* part = p.part + rh * p.nchunk_max * PSTRIDE;
   for (int c = g; c < nchunks; c += TPI) {
-    const float* pc = part + (int64_t)c * PSTRIDE;
-    const float2 ml = *reinterpret_cast<const float2*>(pc);
+    const float* rec = part + (int64_t)c * PSTRIDE;
+    const float2 ml = *reinterpret_cast<const float2*>(rec);
+    const float4* src = reinterpret_cast<const float4*>(rec + kPartPad + j * EPL);
     float ac[EPL];
-    const float4* src = reinterpret_cast<const float4*>(pc + 4 + j * EPL);
 #pragma unroll
     for (int e = 0; e < EPL; e += 4) {
       const float4 x = src[e / 4];
@@ -325,19 +408,18 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     merge_state<EPL>(M, L, A, ml.x, ml.y, ac);
   }
   merge_groups<LPT, EPL>(M, L, A);
-  if (g == 0) write_out<DT, D>(p, o_off, L, A);
+  if (g == 0) write_out<DT>(p, (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh + j, L, A);
 }
 
 // ---------------------------------------------------------------------------
 // Host helpers.
 // ---------------------------------------------------------------------------
-constexpr int kPartPad = 4;
-
 int64_t workspace_bytes(int64_t rows, int64_t heads, int64_t d, int64_t nchunk_max) {
   if (nchunk_max <= 1) return 0;
   return rows * heads * nchunk_max * (d + kPartPad) * (int64_t)sizeof(float);
 }
 
+// Keys one wave covers per sub-chunk for (dtype, head_dim); 0 if unsupported.
 int sub_tokens(int32_t dtype, int32_t d) {
   const int eb = elt_bytes(dtype);
   if (eb == 0 || d <= 0) return 0;
@@ -353,10 +435,19 @@ int sub_tokens(int32_t dtype, int32_t d) {
 int32_t pick_chunk(int32_t rows, int32_t heads, int32_t d, int32_t max_len, int32_t dtype) {
   int sub = sub_tokens(dtype, d);
   if (sub <= 0) sub = 64;
-  // Grow the chunk until the launch holds at most ~16K waves.
-  const int64_t target = 16384;
-  int64_t chunk = sub;
-  while (chunk < max_len && (int64_t)rows * heads * cdiv(max_len, chunk) > target) chunk *= 2;
+  // A chunk is a whole number of workgroup passes (kWaves sub-chunks). Keep
+  // one chunk per (row, head) — no partials, no merge launch — unless there
+  // are too few (row, head) pairs to give every CU ~4 workgroups; then split
+  // the keys just enough to reach that.
+  const int64_t base = (int64_t)kWaves * sub;
+  const int64_t target_wg = 1024;
+  const int64_t rh = (int64_t)rows * heads;
+  const int64_t max_chunks = cdiv(max_len > 0 ? max_len : 1, base);
+  int64_t nchunks = rh >= target_wg ? 1 : cdiv(target_wg, rh > 0 ? rh : 1);
+  nchunks = nchunks < 1 ? 1 : (nchunks > max_chunks ? max_chunks : nchunks);
+  const int64_t per = cdiv(max_len > 0 ? max_len : 1, nchunks);
+  int64_t chunk = cdiv(per, base) * base;
+  if (chunk > 16384) chunk = 16384;
   return (int32_t)chunk;
 }
 
@@ -364,17 +455,19 @@ bool supported_d(int32_t d) { return d == 16 || d == 32 || d == 64 || d == 128; 
 
 template <int DT, int D, bool PAGED>
 void launch_attention(const AttnParams& p, hipStream_t stream) {
-  const int64_t waves = (int64_t)p.nchunk_max * p.batch * p.qlen * p.heads;
-  const int64_t blocks = cdiv(waves, kWavesPerBlock);
-  hipLaunchKernelGGL((attention_kernel<DT, D, PAGED>), dim3((uint32_t)blocks), dim3(64 * kWavesPerBlock), 0, stream, p);
+  const int64_t rh = (int64_t)p.batch * p.qlen * p.heads;
+  hipLaunchKernelGGL((attention_kernel<DT, D, PAGED>), dim3((uint32_t)(rh * p.nchunk_max)), dim3(64 * kWaves), 0,
+                     stream, p);
+  if (p.nchunk_max > 1)
+    hipLaunchKernelGGL((merge_kernel<DT, D>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, stream, p);
 }
 
 template <bool PAGED>
 int dispatch_attention(int32_t dtype, int32_t d, const AttnParams& p, hipStream_t stream) {
-#define SKV_CASE(DT, DD)                          \
-  if (dtype == DT && d == DD) {                   \
-    launch_attention<DT, DD, PAGED>(p, stream);   \
-    return SKV_OK;                                \
+#define SKV_CASE(DT, DD)                        \
+  if (dtype == DT && d == DD) {                 \
+    launch_attention<DT, DD, PAGED>(p, stream); \
+    return SKV_OK;                              \
   }
   SKV_CASE(SKV_F16, 64) SKV_CASE(SKV_BF16, 64) SKV_CASE(SKV_F32, 64)
   SKV_CASE(SKV_F16, 16) SKV_CASE(SKV_BF16, 16) SKV_CASE(SKV_F32, 16)
@@ -389,7 +482,7 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
                       const void* k, const void* v, void* out, int64_t osb, int64_t osq, int64_t osh,
                       const int32_t* lens, int32_t batch, int32_t q_len, int32_t heads, int32_t kv_heads,
                       int32_t d, int32_t max_len, float scale, int32_t causal, int32_t dtype, int32_t chunk,
-                      void* ws, int64_t ws_bytes, int32_t* counters, int64_t counter_count) {
+                      void* ws, int64_t ws_bytes) {
   const int eb = elt_bytes(dtype);
   if (eb == 0) return fail(SKV_EDTYPE, "%s: unknown dtype %d", who, dtype);
   if (!supported_d(d)) return fail(SKV_EINVAL, "%s: head_dim %d not in {16,32,64,128}", who, d);
@@ -408,12 +501,8 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
   const int32_t nchunk_max = max_len > 0 ? (int32_t)cdiv(max_len, chunk) : 1;
   const int64_t need = workspace_bytes((int64_t)batch * q_len, heads, d, nchunk_max);
   if (need > 0 && (!ws || ws_bytes < need || !aligned16(ws)))
-    return fail(SKV_EWORKSPACE, "%s: partials need %lld bytes (16-byte aligned), got %lld", who, (long long)need,
+    return fail(SKV_EWORKSPACE, "%s: workspace needs %lld bytes (16-byte aligned), got %lld", who, (long long)need,
                 (long long)ws_bytes);
-  const int64_t need_cnt = (int64_t)batch * q_len * heads;
-  if (need > 0 && (!counters || counter_count < need_cnt))
-    return fail(SKV_EWORKSPACE, "%s: %lld zeroed int32 counters needed, got %lld", who, (long long)need_cnt,
-                (long long)counter_count);
   p.q = (const uint4*)q;
   p.qsb = qsb / epl;
   p.qsq = qsq / epl;
@@ -435,7 +524,6 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
   p.nchunk_max = nchunk_max;
   p.scale_log2 = scale * kLog2e;
   p.part = need > 0 ? (float*)ws : nullptr;
-  p.counts = need > 0 ? counters : nullptr;
   return SKV_OK;
 }
 
@@ -446,7 +534,7 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
 // ---------------------------------------------------------------------------
 extern "C" {
 
-const char* skv_version(void) { return "speechkv 0.1.0 gfx950"; }
+const char* skv_version(void) { return "speechkv 0.2.0 gfx950"; }
 
 const char* skv_last_error(void) { return g_last_error; }
 
@@ -516,23 +604,38 @@ int32_t skv_default_chunk_tokens(int32_t rows, int32_t num_heads, int32_t head_d
 }
 
 int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
-                        const void* k_pool, const void* v_pool, const int32_t* block_tables, int32_t table_stride,
-                        const int32_t* table_rows, const int32_t* ctx_lens, void* out, int64_t o_stride_b,
-                        int64_t o_stride_q, int64_t o_stride_h, int32_t batch, int32_t q_len, int32_t num_heads,
-                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t num_blocks,
-                        int32_t max_ctx, float scale, int32_t causal, int32_t dtype, int32_t chunk_tokens,
-                        void* partials, int64_t partial_bytes, int32_t* counters, int64_t counter_count,
-                        void* stream) {
-  if (block_size <= 0 || num_blocks < 0 || table_stride <= 0 || !block_tables)
-    return fail(SKV_EINVAL, "skv_paged_attention: bad block table arguments");
+                        void* k_pool, void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                        const int32_t* table_rows, const int32_t* ctx_lens, const void* k_new, const void* v_new,
+                        int64_t new_stride_b, int64_t new_stride_q, int64_t new_stride_h, void* out,
+                        int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h, int32_t batch, int32_t q_len,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int32_t num_blocks, int32_t max_ctx, float scale, int32_t causal, int32_t dtype,
+                        int32_t chunk_tokens, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (block_size < 2 || num_blocks < 0 || table_stride <= 0 || !block_tables)
+    return fail(SKV_EINVAL, "skv_paged_attention: bad block table arguments (block_size must be >= 2)");
+  if ((k_new == nullptr) != (v_new == nullptr))
+    return fail(SKV_EINVAL, "skv_paged_attention: k_new and v_new must both be given or both be NULL");
   const int64_t table_cap = (int64_t)table_stride * block_size;
   if (max_ctx > table_cap) max_ctx = (int32_t)table_cap;
   AttnParams p{};
   int rc = prepare_attention(p, "skv_paged_attention", q, q_stride_b, q_stride_q, q_stride_h, k_pool, v_pool, out,
                              o_stride_b, o_stride_q, o_stride_h, ctx_lens, batch, q_len, num_heads, num_kv_heads,
-                             head_dim, max_ctx, scale, causal, dtype, chunk_tokens, partials, partial_bytes,
-                             counters, counter_count);
+                             head_dim, max_ctx, scale, causal, dtype, chunk_tokens, workspace, workspace_bytes);
   if (rc != SKV_OK) return rc;
+  if (p.chunk / block_size + 2 > kMaxChunkBlocks)
+    return fail(SKV_EINVAL, "skv_paged_attention: chunk_tokens %d spans more than %d blocks of %d", p.chunk,
+                kMaxChunkBlocks - 2, block_size);
+  if (k_new) {
+    const int epl = 16 / elt_bytes(dtype);
+    if (!aligned16(k_new) || !aligned16(v_new) || new_stride_b % epl || new_stride_q % epl || new_stride_h % epl)
+      return fail(SKV_EALIGN, "skv_paged_attention: k_new/v_new must be 16-byte aligned with strides in %d-element units",
+                  epl);
+    p.kn = (const uint4*)k_new;
+    p.vn = (const uint4*)v_new;
+    p.nsb = new_stride_b / epl;
+    p.nsq = new_stride_q / epl;
+    p.nsh = new_stride_h / epl;
+  }
   if (batch == 0) return SKV_OK;
   p.tables = block_tables;
   p.tstride = table_stride;
@@ -550,12 +653,11 @@ int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
                         const int32_t* slot_ids, const int32_t* lens, void* out, int64_t o_stride_b,
                         int64_t o_stride_q, int64_t o_stride_h, int32_t batch, int32_t q_len, int32_t num_heads,
                         int32_t num_kv_heads, int32_t head_dim, int32_t max_len, float scale, int32_t causal,
-                        int32_t dtype, int32_t chunk_tokens, void* partials, int64_t partial_bytes,
-                        int32_t* counters, int64_t counter_count, void* stream) {
+                        int32_t dtype, int32_t chunk_tokens, void* workspace, int64_t workspace_bytes, void* stream) {
   AttnParams p{};
   int rc = prepare_attention(p, "skv_dense_attention", q, q_stride_b, q_stride_q, q_stride_h, k, v, out, o_stride_b,
                              o_stride_q, o_stride_h, lens, batch, q_len, num_heads, num_kv_heads, head_dim, max_len,
-                             scale, causal, dtype, chunk_tokens, partials, partial_bytes, counters, counter_count);
+                             scale, causal, dtype, chunk_tokens, workspace, workspace_bytes);
   if (rc != SKV_OK) return rc;
   const int epl = 16 / elt_bytes(dtype);
   if (kv_stride_s % epl || kv_stride_h % epl || kv_stride_t % epl)

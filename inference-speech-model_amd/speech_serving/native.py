@@ -36,13 +36,13 @@ SIGNATURES = {
                             _c_i32, _c_i32, _c_p]),
     "skv_attention_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "skv_default_chunk_tokens": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
-    "skv_paged_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p,
+    "skv_paged_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p,
+                                     _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p,
                                      _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
-                                     _c_i32, _c_i32, _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_i64,
-                                     _c_p]),
+                                     _c_i32, _c_i32, _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p]),
     "skv_dense_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p,
                                      _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
-                                     _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p, _c_i64, _c_p]),
+                                     _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p]),
 }
 
 
@@ -110,12 +110,10 @@ def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# Split-K scratch, one pair per device: `partials` (any content) and
-# `counters` (int32, zero-filled once, used for arrival counters only; every
-# attention launch leaves them zero). Both grow only outside graph capture.
+# Split-K workspace: one buffer per device (fp32 partials; any content on
+# entry), grown only outside graph capture.
 # ---------------------------------------------------------------------------
-_partials: Dict[int, torch.Tensor] = {}
-_counters: Dict[int, torch.Tensor] = {}
+_workspaces: Dict[int, torch.Tensor] = {}
 
 
 def _dev_index(device) -> int:
@@ -123,43 +121,32 @@ def _dev_index(device) -> int:
     return torch.cuda.current_device() if idx is None else idx
 
 
-def reserve_workspace(partial_bytes: int, counter_count: int, device) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Return (partials uint8, counters int32) of at least the requested sizes."""
+def reserve_workspace(nbytes: int, device) -> torch.Tensor:
+    """Return the device's workspace, grown to at least `nbytes`."""
     idx = _dev_index(device)
-    part = _partials.get(idx)
-    cnt = _counters.get(idx)
-    grow_p = part is None or part.numel() < partial_bytes
-    grow_c = cnt is None or cnt.numel() < counter_count
-    if grow_p or grow_c:
+    ws = _workspaces.get(idx)
+    if ws is None or ws.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError(
-                f"attention scratch ({partial_bytes} B partials, {counter_count} counters) must be reserved "
-                "before graph capture")
-        dev = torch.device("cuda", idx)
-        if grow_p:
-            size = max(int(partial_bytes), 1 << 20, 0 if part is None else 2 * part.numel())
-            part = torch.empty(size, dtype=torch.uint8, device=dev)
-            _partials[idx] = part
-        if grow_c:
-            size = max(int(counter_count), 4096, 0 if cnt is None else 2 * cnt.numel())
-            cnt = torch.zeros(size, dtype=torch.int32, device=dev)
-            _counters[idx] = cnt
-    return part, cnt
+            raise RuntimeError(f"attention workspace of {nbytes} bytes must be reserved before graph capture")
+        size = max(int(nbytes), 1 << 20, 0 if ws is None else 2 * ws.numel())
+        ws = torch.empty(size, dtype=torch.uint8, device=torch.device("cuda", idx))
+        _workspaces[idx] = ws
+    return ws
 
 
 def reserve_attention(rows: int, heads: int, head_dim: int, max_len: int, dtype: torch.dtype, device,
                       chunk_tokens: int = 0) -> None:
-    """Pre-size the scratch for an attention call shape (call before graph capture)."""
+    """Pre-size the workspace for an attention call shape (call before graph capture)."""
     need = attention_workspace_bytes(rows, heads, head_dim, max(max_len, 1), dtype, chunk_tokens)
     if need > 0:
-        reserve_workspace(need, rows * heads, device)
+        reserve_workspace(need, device)
 
 
-def _scratch(rows: int, heads: int, need: int, device):
+def _scratch(need: int, device):
     if need <= 0:
-        return None, 0, None, 0
-    part, cnt = reserve_workspace(need, rows * heads, device)
-    return part.data_ptr(), part.numel(), cnt.data_ptr(), cnt.numel()
+        return None, 0
+    ws = reserve_workspace(need, device)
+    return ws.data_ptr(), ws.numel()
 
 
 def attention_workspace_bytes(rows: int, heads: int, head_dim: int, max_len: int, dtype: torch.dtype,
@@ -267,13 +254,18 @@ def _q4(q: torch.Tensor, name: str) -> torch.Tensor:
 def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
                     ctx_lens: torch.Tensor, max_ctx: int, scale: float, causal: bool = False,
                     table_rows: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-                    chunk_tokens: int = 0) -> torch.Tensor:
+                    chunk_tokens: int = 0, k_new: Optional[torch.Tensor] = None,
+                    v_new: Optional[torch.Tensor] = None) -> torch.Tensor:
     """softmax(q K^T * scale) V over each row's paged K/V.
 
     q: [B, H, D] or [B, Q, H, D]; pools [num_blocks, BS, Hkv, D]; block_tables
     int32 [*, max_blocks]; ctx_lens int32 [B] = keys visible to the last query
     (new token included); causal: query qi sees ctx_lens[b] - (Q - 1 - qi) keys.
-    Reference math: speech_serving/models.py:126-165 and :444-466.
+    With k_new/v_new ([B, Q, Hkv, D] or [B, Hkv, D]) the Q newest keys
+    (positions ctx_lens[b]-Q .. ctx_lens[b]-1) are appended into the pools
+    through the block table in the same launch.
+    Reference math: speech_serving/models.py:126-165 and :444-466; append:
+    speech_serving/phase_aware_scheduler.py:1004-1010.
     """
     for t, n in ((q, "q"), (k_pool, "k_pool"), (v_pool, "v_pool")):
         _gpu(t, n)
@@ -305,13 +297,29 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     max_ctx = max(0, min(int(max_ctx), block_tables.shape[1] * bs))
     if chunk_tokens <= 0:
         chunk_tokens = default_chunk_tokens(bsz * qlen, heads, d, max(max_ctx, 1), q4.dtype)
+    kn4 = vn4 = None
+    nstr = (0, 0, 0)
+    if (k_new is None) != (v_new is None):
+        raise RuntimeError("paged_attention: k_new and v_new must both be given or both be None")
+    if k_new is not None:
+        _gpu(k_new, "k_new")
+        _gpu(v_new, "v_new")
+        kn4, vn4 = _q4(k_new, "k_new"), _q4(v_new, "v_new")
+        if tuple(kn4.shape) != (bsz, qlen, hkv, d) or tuple(vn4.shape) != (bsz, qlen, hkv, d):
+            raise RuntimeError(f"paged_attention: k_new/v_new must be [{bsz}, {qlen}, {hkv}, {d}]")
+        if kn4.dtype != k_pool.dtype or vn4.dtype != k_pool.dtype:
+            raise RuntimeError("paged_attention: k_new/v_new dtype must match the pool")
+        if kn4.stride(3) != 1 or vn4.stride(3) != 1 or kn4.stride() != vn4.stride():
+            kn4, vn4 = kn4.contiguous(), vn4.contiguous()
+        nstr = (kn4.stride(0), kn4.stride(1), kn4.stride(2))
     need = attention_workspace_bytes(bsz * qlen, heads, d, max_ctx, q4.dtype, chunk_tokens)
-    pp, pn, cp, cn = _scratch(bsz * qlen, heads, need, q.device)
+    wp, wn = _scratch(need, q.device)
     rc = lib().skv_paged_attention(
         q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2), k_pool.data_ptr(), v_pool.data_ptr(),
         block_tables.data_ptr(), block_tables.stride(0), _ptr(table_rows), ctx_lens.data_ptr(),
+        _ptr(kn4), _ptr(vn4), nstr[0], nstr[1], nstr[2],
         o4.data_ptr(), o4.stride(0), o4.stride(1), o4.stride(2), bsz, qlen, heads, hkv, d, bs, nb, max_ctx,
-        float(scale), 1 if causal else 0, code, chunk_tokens, pp, pn, cp, cn, _stream(q.device))
+        float(scale), 1 if causal else 0, code, chunk_tokens, wp, wn, _stream(q.device))
     _check(rc, "skv_paged_attention")
     return out
 
@@ -355,11 +363,11 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: tor
     if chunk_tokens <= 0:
         chunk_tokens = default_chunk_tokens(bsz * qlen, heads, d, max(max_len, 1), q4.dtype)
     need = attention_workspace_bytes(bsz * qlen, heads, d, max_len, q4.dtype, chunk_tokens)
-    pp, pn, cp, cn = _scratch(bsz * qlen, heads, need, q.device)
+    wp, wn = _scratch(need, q.device)
     rc = lib().skv_dense_attention(
         q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2), k.data_ptr(), v.data_ptr(),
         k.stride(0), k.stride(1), k.stride(2), _ptr(slot_ids), lens.data_ptr(), o4.data_ptr(),
         o4.stride(0), o4.stride(1), o4.stride(2), bsz, qlen, heads, hkv, d, max_len, float(scale),
-        1 if causal else 0, _code(q4.dtype), chunk_tokens, pp, pn, cp, cn, _stream(q.device))
+        1 if causal else 0, _code(q4.dtype), chunk_tokens, wp, wn, _stream(q.device))
     _check(rc, "skv_dense_attention")
     return out

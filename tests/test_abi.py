@@ -52,13 +52,15 @@ def test_workspace_bytes_formula():
 
 def test_default_chunk():
     lib = native.lib()
-    # fp16 D=64: 8 rows per wave instruction x 8 unrolled = 64-key sub-chunk
-    assert lib.skv_default_chunk_tokens(64, 32, 64, 448, native.SKV_F16) == 64
-    # many long rows: chunk grows until <= 16K waves
-    c = lib.skv_default_chunk_tokens(64, 20, 64, 1500, native.SKV_BF16)
-    assert c % 64 == 0 and 64 * 20 * -(-1500 // c) <= 16384
-    # fp32 D=64: 4 rows per instruction x 8 = 32
-    assert lib.skv_default_chunk_tokens(1, 1, 64, 10, native.SKV_F32) == 32
+    # Enough (row, head) pairs to fill the GPU: one chunk covering every key,
+    # rounded up to whole 4-wave passes (fp16 D=64: 4 waves x 64 keys = 256).
+    assert lib.skv_default_chunk_tokens(64, 32, 64, 448, native.SKV_F16) == 512
+    assert lib.skv_default_chunk_tokens(64, 20, 64, 1500, native.SKV_BF16) == 1536
+    # Few pairs: split the keys so that ~1024 workgroups run.
+    c = lib.skv_default_chunk_tokens(1, 20, 64, 1500, native.SKV_BF16)
+    assert c == 256 and 20 * -(-1500 // c) <= 1024
+    # fp32 D=64: 4 rows x 8 = 32 keys per wave -> 128-key passes
+    assert lib.skv_default_chunk_tokens(1, 1, 64, 10, native.SKV_F32) == 128
 
 
 FAKE = 1 << 20  # aligned, never dereferenced: validation fails before any launch
@@ -78,28 +80,27 @@ def test_append_rejects_misaligned_stride():
 
 def test_attention_rejects_unsupported_head_dim():
     lib = native.lib()
-    rc = lib.skv_paged_attention(FAKE, 48, 48, 48, FAKE, FAKE, FAKE, 4, None, FAKE, FAKE, 48, 48, 48,
-                                 1, 1, 1, 1, 48, 16, 8, 64, 1.0, 0, native.SKV_F16, 0, None, 0, None, 0, None)
+    rc = lib.skv_paged_attention(FAKE, 48, 48, 48, FAKE, FAKE, FAKE, 4, None, FAKE, None, None, 0, 0, 0,
+                                 FAKE, 48, 48, 48,
+                                 1, 1, 1, 1, 48, 16, 8, 64, 1.0, 0, native.SKV_F16, 0, None, 0, None)
     assert rc == -1 and b"head_dim" in lib.skv_last_error()
 
 
 def test_attention_requires_workspace_for_split_keys():
     lib = native.lib()
     rc = lib.skv_dense_attention(FAKE, 64, 64, 64, FAKE, FAKE, 64 * 1500, 64 * 1500, 64, None, FAKE, FAKE,
-                                 64, 64, 64, 4, 1, 1, 1, 64, 1500, 0.125, 0, native.SKV_F16, 64, None, 0, None, 0,
-                                 None)
-    assert rc == -4 and b"partials" in lib.skv_last_error()
-    # partials present but counters missing
+                                 64, 64, 64, 4, 1, 1, 1, 64, 1500, 0.125, 0, native.SKV_F16, 64, None, 0, None)
+    assert rc == -4 and b"workspace" in lib.skv_last_error()
+    # too small
     rc = lib.skv_dense_attention(FAKE, 64, 64, 64, FAKE, FAKE, 64 * 1500, 64 * 1500, 64, None, FAKE, FAKE,
-                                 64, 64, 64, 4, 1, 1, 1, 64, 1500, 0.125, 0, native.SKV_F16, 64, FAKE, 1 << 30, None,
-                                 0, None)
-    assert rc == -4 and b"counters" in lib.skv_last_error()
+                                 64, 64, 64, 4, 1, 1, 1, 64, 1500, 0.125, 0, native.SKV_F16, 64, FAKE, 64, None)
+    assert rc == -4
 
 
 def test_attention_rejects_bad_group():
     lib = native.lib()
     rc = lib.skv_dense_attention(FAKE, 64, 64, 64, FAKE, FAKE, 64, 64, 64, None, FAKE, FAKE, 64, 64, 64,
-                                 1, 1, 3, 2, 64, 10, 0.125, 0, native.SKV_F16, 0, None, 0, None, 0, None)
+                                 1, 1, 3, 2, 64, 10, 0.125, 0, native.SKV_F16, 0, None, 0, None)
     assert rc == -1
 
 

@@ -169,7 +169,7 @@ def test_paged_attention_config2_full_size(cuda):
 
 
 @pytest.mark.parametrize("chunk", [64, 128, 256, 512])
-def test_paged_attention_split_sizes_agree_and_counters_reset(cuda, chunk):
+def test_paged_attention_split_sizes_agree_and_repeat(cuda, chunk):
     gen = torch.Generator().manual_seed(5)
     bsz, h, d, bs, nb = 16, 8, 64, 16, 1024
     ctx = torch.randint(1, 449, (bsz,), generator=gen).to(torch.int32)
@@ -178,7 +178,7 @@ def test_paged_attention_split_sizes_agree_and_counters_reset(cuda, chunk):
     q = torch.randn(bsz, h, d, generator=gen).to(cuda, torch.bfloat16)
     args = (q, kp, vp, tables.to(cuda), ctx.to(cuda), 448, 0.125)
     a = native.paged_attention(*args, chunk_tokens=chunk)
-    b = native.paged_attention(*args, chunk_tokens=chunk)  # counters must be back at zero
+    b = native.paged_attention(*args, chunk_tokens=chunk)  # deterministic merge order
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     want = O.paged_attention(f64(q)[:, None], f64(kp), f64(vp), tables.numpy(), ctx.tolist(), 0.125)[:, 0]
