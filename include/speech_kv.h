@@ -29,6 +29,10 @@
  *                         (eager) and :468-479 (graph), with the masks of
  *                         phase_aware_scheduler.py:884-887,964-970 and
  *                         graph_decode_buffers.py:529,537 expressed as lengths.
+ *   skv_argmax            greedy sampling (first maximum) with optional on-device
+ *                         token feedback per decode slot. Replaces argmax +
+ *                         copy_ at speech_serving/models.py:486-487 and
+ *                         graph_decode_buffers.py:463.
  *
  * Conventions
  *   - Every pointer argument is a device pointer owned by the caller (PyTorch).
@@ -107,6 +111,21 @@ SKV_API int skv_gather(const void* k_pool, const void* v_pool,
                int32_t batch, int32_t num_heads, int32_t head_dim,
                int32_t block_size, int32_t num_blocks, int32_t max_len,
                int32_t dtype, void* stream);
+
+/*
+ * skv_argmax — greedy token per row: the first index of the maximum of
+ * logits[r, 0:vocab] (a NaN counts as the maximum), as torch.argmax(dim=-1).
+ *   logits     : [rows, row_stride] of dtype, row_stride >= vocab
+ *   out_tokens : int64 [rows]
+ *   row_slots, slot_tokens (optional, both or neither): also store the token
+ *                at slot_tokens[row_slots[r]] (skipped for a negative slot) —
+ *                the on-device token feedback of a graph decode step.
+ * Reference: speech_serving/models.py:486-487; phase_aware_scheduler.py:693,
+ * 997, 1026.
+ */
+SKV_API int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
+                       int32_t dtype, int64_t* out_tokens, const int32_t* row_slots,
+                       int64_t* slot_tokens, void* stream);
 
 /*
  * Workspace bytes needed by skv_paged_attention / skv_dense_attention for a

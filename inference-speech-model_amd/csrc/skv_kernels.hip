@@ -118,6 +118,78 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint4* __restrict__ k
 }
 
 // ---------------------------------------------------------------------------
+// Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
+// (NaN counts as the maximum, as in torch.argmax). Optionally also writes the
+// token to slot_tokens[row_slots[r]] (skipped when the slot is negative).
+// One 256-thread workgroup per row.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool argmax_better(float v1, int i1, float v2, int i2) {
+  const bool n1 = v1 != v1, n2 = v2 != v2;
+  if (n1 || n2) return n1 && (!n2 || i1 < i2);
+  return v1 > v2 || (v1 == v2 && i1 < i2);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_logit(const void* row, int i);
+template <> __device__ __forceinline__ float load_logit<SKV_F32>(const void* row, int i) {
+  return ((const float*)row)[i];
+}
+template <> __device__ __forceinline__ float load_logit<SKV_F16>(const void* row, int i) {
+  return (float)((const _Float16*)row)[i];
+}
+template <> __device__ __forceinline__ float load_logit<SKV_BF16>(const void* row, int i) {
+  return __uint_as_float((uint32_t)((const uint16_t*)row)[i] << 16);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void argmax_kernel(const char* __restrict__ logits, int64_t row_bytes,
+                                                     int32_t vocab, int64_t* __restrict__ out,
+                                                     const int32_t* __restrict__ row_slots,
+                                                     int64_t* __restrict__ slot_tokens) {
+  __shared__ float s_v[4];
+  __shared__ int s_i[4];
+  const int r = blockIdx.x;
+  const char* row = logits + (int64_t)r * row_bytes;
+  float best = kNegInf;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < vocab; i += 256) {
+    const float v = load_logit<DT>(row, i);
+    if (argmax_better(v, i, best, bi)) {
+      best = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float v2 = __shfl_xor(best, off, 64);
+    const int i2 = __shfl_xor(bi, off, 64);
+    if (argmax_better(v2, i2, best, bi)) {
+      best = v2;
+      bi = i2;
+    }
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_v[wave] = best;
+    s_i[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w)
+      if (argmax_better(s_v[w], s_i[w], best, bi)) {
+        best = s_v[w];
+        bi = s_i[w];
+      }
+    const int64_t tok = bi == 0x7fffffff ? 0 : bi;
+    out[r] = tok;
+    if (row_slots) {
+      const int slot = row_slots[r];
+      if (slot >= 0) slot_tokens[slot] = tok;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Attention.
 // ---------------------------------------------------------------------------
 #ifndef SKV_ATTN_WAVES
@@ -590,6 +662,35 @@ int skv_gather(const void* k_pool, const void* v_pool, const int32_t* block_tabl
                      (uint4*)k_out, (uint4*)(v_out ? v_out : k_out), batch, num_heads, vpr, block_size, num_blocks,
                      max_len);
   return check_launch("skv_gather");
+}
+
+int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab, int32_t dtype,
+               int64_t* out_tokens, const int32_t* row_slots, int64_t* slot_tokens, void* stream) {
+  const int eb = elt_bytes(dtype);
+  if (eb == 0) return fail(SKV_EDTYPE, "skv_argmax: unknown dtype %d", dtype);
+  if (rows < 0 || vocab <= 0 || row_stride < vocab)
+    return fail(SKV_EINVAL, "skv_argmax: bad sizes rows=%d vocab=%d row_stride=%lld", rows, vocab,
+                (long long)row_stride);
+  if (rows == 0) return SKV_OK;
+  if (!logits || !out_tokens || ((row_slots == nullptr) != (slot_tokens == nullptr)))
+    return fail(SKV_EINVAL, "skv_argmax: null pointer argument");
+  const int64_t rb = row_stride * eb;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case SKV_F32:
+      hipLaunchKernelGGL(argmax_kernel<SKV_F32>, dim3(rows), dim3(256), 0, s, (const char*)logits, rb, vocab,
+                         out_tokens, row_slots, slot_tokens);
+      break;
+    case SKV_F16:
+      hipLaunchKernelGGL(argmax_kernel<SKV_F16>, dim3(rows), dim3(256), 0, s, (const char*)logits, rb, vocab,
+                         out_tokens, row_slots, slot_tokens);
+      break;
+    default:
+      hipLaunchKernelGGL(argmax_kernel<SKV_BF16>, dim3(rows), dim3(256), 0, s, (const char*)logits, rb, vocab,
+                         out_tokens, row_slots, slot_tokens);
+      break;
+  }
+  return check_launch("skv_argmax");
 }
 
 int64_t skv_attention_workspace_bytes(int32_t rows, int32_t num_heads, int32_t head_dim, int32_t max_len,

@@ -1,0 +1,424 @@
+"""Whisper-class encoder-decoder model whose attention runs on the gfx950 kernels.
+
+Same module structure and parameter names as the reference's
+WhisperClassSpeechEncoderDecoderModel / DecoderLayer
+(speech_serving/models.py:79-208, 298-487), so a reference state_dict loads
+unchanged:
+    DecoderLayer: self_attn_{q,k,v,out}, cross_attn_{q,k,v,out} (bias-free),
+                  norm1/norm2/norm3 (LayerNorm), mlp = Linear-GELU-Linear.
+    Model:        conv1, conv2, encoder_layers, encoder_norm, decoder_embed,
+                  decoder_layers, decoder_norm, lm_head.
+Semantics kept from the reference: pre-LN residual blocks; self-attention
+scale head_dim^-1/2; causal mask for multi-token decoder inputs; cross-
+attention only for layers that receive encoder K/V or hidden states, and
+then the MLP normalises with norm3 (else norm2); no positional embedding.
+
+Entry points:
+    encode(mel) -> (hidden, [(K, V)] per encoder layer)        models.py:349-367
+    decode_step(...)  contiguous past KV, reference signature   models.py:369-423
+    decode_step_graph_fixed(...) bucketed static KV signature   models.py:425-487
+    decode_step_paged(ids, PagedKV, CrossKV)  the paged hot path: per layer one
+        fused launch appends the new K/V through the block table and attends,
+        and one launch attends the slot's contiguous encoder K/V.
+    project_cross_kv(hidden) -> [(K, V)] per decoder layer via cross_attn_k/v.
+Every attention, append and greedy step is a HIP kernel (speech_serving.native);
+tensors must live on the GPU.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any, List, Optional, Sequence, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import native
+
+
+# ---------------------------------------------------------------------------
+# KV containers.
+# ---------------------------------------------------------------------------
+class LayerKV:
+    """One layer's contiguous self-attention K/V ([B, H, T, D]), shaped like the
+    cache layers the reference returns (`.keys`, `.values`)."""
+
+    def __init__(self, keys: torch.Tensor, values: torch.Tensor):
+        self.keys = keys
+        self.values = values
+        self.is_initialized = True
+
+
+class KVCache:
+    """List of LayerKV, exposed as `.layers` like the reference's DynamicCache."""
+
+    def __init__(self, layers: Optional[List[LayerKV]] = None):
+        self.layers: List[LayerKV] = layers or []
+
+    def __len__(self) -> int:
+        return len(self.layers)
+
+    def to_legacy_cache(self):
+        return tuple((l.keys, l.values) for l in self.layers)
+
+
+class ModelOutput:
+    def __init__(self, logits: torch.Tensor, past_key_values: Optional[KVCache]):
+        self.logits = logits
+        self.past_key_values = past_key_values
+
+
+@dataclass
+class PagedKV:
+    """Self-attention K/V that lives in a BlockManager pool.
+
+    block_tables: int32 [R, max_blocks]; row b uses table row table_rows[b]
+    (or b). ctx_lens: int32 [B] = keys of row b including its new tokens.
+    max_ctx bounds ctx_lens (launch grid size).
+    """
+    k_pools: Sequence[torch.Tensor]
+    v_pools: Sequence[torch.Tensor]
+    block_tables: torch.Tensor
+    ctx_lens: torch.Tensor
+    max_ctx: int
+    table_rows: Optional[torch.Tensor] = None
+
+
+@dataclass
+class CrossKV:
+    """Encoder K/V per decoder layer as [S, H, T, D] views (slot-major buffer);
+    row b reads slot slot_ids[b] (or b) over its first lens[b] positions.
+    Layers at or beyond len(k) get no cross-attention (models.py:398-406)."""
+    k: Sequence[torch.Tensor]
+    v: Sequence[torch.Tensor]
+    lens: torch.Tensor
+    max_len: int
+    slot_ids: Optional[torch.Tensor] = None
+
+    def has(self, layer: int) -> bool:
+        return layer < len(self.k)
+
+
+# ---------------------------------------------------------------------------
+# Mask handling for the reference's contiguous API.
+# ---------------------------------------------------------------------------
+def _keep_mask(mask: torch.Tensor, batch: int, t: int) -> torch.Tensor:
+    """Reference masks (models.py:142-157, 186-199) as a bool keep-mask [B, T].
+
+    bool: True = attend. Binary 0/1 integers: 1 = attend. Additive floats:
+    0 = attend, <= -1000 = masked (the reference uses -10000 and finfo.min);
+    other additive values are a bias these kernels do not apply.
+    """
+    m = mask
+    while m.dim() > 2:
+        if m.shape[1] != 1:
+            if not bool((m == m[:, :1]).all()):
+                raise NotImplementedError("per-head / per-query attention masks are not supported")
+            m = m[:, :1]
+        m = m[:, 0]
+    m = m.expand(batch, t) if m.shape[0] == 1 else m
+    if m.dtype == torch.bool:
+        return m
+    if not m.is_floating_point() or bool(torch.isin(m, torch.tensor([0, 1], device=m.device)).all()):
+        return m != 0
+    keep = m == 0
+    if not bool((keep | (m <= -1000)).all()):
+        raise NotImplementedError("additive attention bias other than 0 / large-negative masking")
+    return keep
+
+
+def _compact(k: torch.Tensor, v: torch.Tensor, keep: torch.Tensor):
+    """Move each row's kept positions to the front (order preserved); returns K, V, lens."""
+    lens = keep.sum(dim=-1).to(torch.int32)
+    if bool((keep == (torch.arange(keep.shape[1], device=keep.device)[None] < lens[:, None])).all()):
+        return k, v, lens  # already a prefix mask
+    order = torch.argsort((~keep).to(torch.int8), dim=-1, stable=True)
+    idx = order[:, None, :, None].expand(k.shape[0], k.shape[1], k.shape[2], k.shape[3])
+    return torch.gather(k, 2, idx).contiguous(), torch.gather(v, 2, idx).contiguous(), lens
+
+
+# ---------------------------------------------------------------------------
+# Layers.
+# ---------------------------------------------------------------------------
+class DecoderLayer(nn.Module):
+    """Pre-LN transformer layer with self-attention, optional cross-attention and a GELU MLP."""
+
+    def __init__(self, hidden_dim: int, num_heads: int, head_dim: int, is_decoder: bool = True):
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.is_decoder = is_decoder
+        hd = num_heads * head_dim
+        self.self_attn_q = nn.Linear(hidden_dim, hd, bias=False)
+        self.self_attn_k = nn.Linear(hidden_dim, hd, bias=False)
+        self.self_attn_v = nn.Linear(hidden_dim, hd, bias=False)
+        self.self_attn_out = nn.Linear(hd, hidden_dim, bias=False)
+        self.cross_attn_q = nn.Linear(hidden_dim, hd, bias=False)
+        self.cross_attn_k = nn.Linear(hidden_dim, hd, bias=False)
+        self.cross_attn_v = nn.Linear(hidden_dim, hd, bias=False)
+        self.cross_attn_out = nn.Linear(hd, hidden_dim, bias=False)
+        self.norm1 = nn.LayerNorm(hidden_dim)
+        self.norm2 = nn.LayerNorm(hidden_dim)
+        self.norm3 = nn.LayerNorm(hidden_dim)
+        self.mlp = nn.Sequential(nn.Linear(hidden_dim, hidden_dim * 4), nn.GELU(),
+                                 nn.Linear(hidden_dim * 4, hidden_dim))
+        self._qkv_key = None
+        self._qkv_w: Optional[torch.Tensor] = None
+
+    @property
+    def scale(self) -> float:
+        return 1.0 / math.sqrt(self.head_dim)
+
+    def qkv_weight(self) -> torch.Tensor:
+        """[3*H*D, hidden] concatenation of the q/k/v weights, rebuilt when any of them changes."""
+        ws = (self.self_attn_q.weight, self.self_attn_k.weight, self.self_attn_v.weight)
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
+        if key != self._qkv_key:
+            if ws[0].is_cuda and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("fused q/k/v weight must be built before graph capture (run one eager step)")
+            self._qkv_w = torch.cat([w.detach() for w in ws], dim=0).contiguous()
+            self._qkv_key = key
+        return self._qkv_w
+
+    def _qkv(self, x: torch.Tensor):
+        b, s, _ = x.shape
+        hd = self.num_heads * self.head_dim
+        qkv = F.linear(self.norm1(x), self.qkv_weight())
+        shape = (b, s, self.num_heads, self.head_dim)
+        return qkv[..., :hd].view(shape), qkv[..., hd:2 * hd].view(shape), qkv[..., 2 * hd:].view(shape)
+
+    def _finish(self, x: torch.Tensor, cross_used: bool) -> torch.Tensor:
+        norm = self.norm3 if cross_used else self.norm2
+        return x + self.mlp(norm(x))
+
+    def _cross_q(self, x: torch.Tensor) -> torch.Tensor:
+        b, s, _ = x.shape
+        return self.cross_attn_q(self.norm2(x)).view(b, s, self.num_heads, self.head_dim)
+
+    # -- paged hot path ---------------------------------------------------------
+    def forward_paged(self, x: torch.Tensor, layer: int, kv: PagedKV, cross: Optional[CrossKV]) -> torch.Tensor:
+        b, s, _ = x.shape
+        hd = self.num_heads * self.head_dim
+        q, k, v = self._qkv(x)
+        attn = native.paged_attention(q, kv.k_pools[layer], kv.v_pools[layer], kv.block_tables, kv.ctx_lens,
+                                      kv.max_ctx, self.scale, causal=s > 1, table_rows=kv.table_rows,
+                                      k_new=k, v_new=v)
+        x = x + self.self_attn_out(attn.view(b, s, hd))
+        used = cross is not None and cross.has(layer)
+        if used:
+            c = native.dense_attention(self._cross_q(x), cross.k[layer], cross.v[layer], cross.lens,
+                                       cross.max_len, self.scale, slot_ids=cross.slot_ids)
+            x = x + self.cross_attn_out(c.view(b, s, hd))
+        return self._finish(x, used)
+
+    # -- contiguous API of the reference (models.py:110-208) ---------------------
+    def forward(self, x: torch.Tensor, past_key_values: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+                encoder_hidden_states: Optional[torch.Tensor] = None,
+                encoder_past_kv: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+                attention_mask: Optional[torch.Tensor] = None,
+                encoder_attention_mask: Optional[torch.Tensor] = None):
+        b, s, _ = x.shape
+        hd = self.num_heads * self.head_dim
+        q, k, v = self._qkv(x)
+        k = k.transpose(1, 2)
+        v = v.transpose(1, 2)
+        if past_key_values is not None:
+            pk, pv = past_key_values
+            k = torch.cat([pk.to(q.dtype), k], dim=2)
+            v = torch.cat([pv.to(q.dtype), v], dim=2)
+        else:
+            k, v = k.contiguous(), v.contiguous()
+        new_past = (k, v)
+        t = k.shape[2]
+        if attention_mask is not None:
+            kk, vv, lens = _compact(k, v, _keep_mask(attention_mask, b, t))
+        else:
+            kk, vv = k, v
+            lens = torch.full((b,), t, dtype=torch.int32, device=x.device)
+        attn = native.dense_attention(q, kk, vv, lens, t, self.scale, causal=self.is_decoder and s > 1)
+        x = x + self.self_attn_out(attn.reshape(b, s, hd))
+
+        new_cross = None
+        used = encoder_hidden_states is not None or encoder_past_kv is not None
+        if used:
+            if encoder_past_kv is not None:
+                ck, cv = encoder_past_kv
+                ck, cv = ck.to(q.dtype), cv.to(q.dtype)
+            else:
+                enc = encoder_hidden_states
+                te = enc.shape[1]
+                ck = self.cross_attn_k(enc).view(b, te, self.num_heads, self.head_dim).transpose(1, 2)
+                cv = self.cross_attn_v(enc).view(b, te, self.num_heads, self.head_dim).transpose(1, 2)
+            new_cross = (ck, cv)
+            if ck.stride(3) != 1 or ck.stride() != cv.stride():
+                ck, cv = ck.contiguous(), cv.contiguous()
+            te = ck.shape[2]
+            if encoder_attention_mask is not None:
+                ck, cv, clens = _compact(ck, cv, _keep_mask(encoder_attention_mask, b, te))
+            else:
+                clens = torch.full((b,), te, dtype=torch.int32, device=x.device)
+            if ck.shape[0] == 1 and b > 1:
+                ck, cv = ck.expand(b, -1, -1, -1), cv.expand(b, -1, -1, -1)
+            c = native.dense_attention(self._cross_q(x), ck, cv, clens, te, self.scale)
+            x = x + self.cross_attn_out(c.reshape(b, s, hd))
+        return self._finish(x, used), new_past, new_cross
+
+
+# ---------------------------------------------------------------------------
+# Model.
+# ---------------------------------------------------------------------------
+class WhisperClassSpeechEncoderDecoderModel(nn.Module):
+    """Conv front-end + encoder layers + causal decoder with cross-attention."""
+
+    def __init__(self, num_encoder_layers: int = 4, num_decoder_layers: int = 4, num_heads: int = 4,
+                 hidden_dim: int = 256, mel_dim: int = 80, vocab_size: int = 51200,
+                 head_dim: Optional[int] = None):
+        super().__init__()
+        self.num_encoder_layers = num_encoder_layers
+        self.num_decoder_layers = num_decoder_layers
+        self.num_heads = num_heads
+        self.head_dim = head_dim if head_dim is not None else hidden_dim // num_heads
+        self.hidden_dim = hidden_dim
+        self.vocab_size = vocab_size
+
+        class Config:
+            pass
+
+        self.config = Config()
+        self.config.num_hidden_layers = num_decoder_layers
+        self.config.num_attention_heads = num_heads
+        self.config.num_key_value_heads = num_heads
+        self.config.hidden_size = hidden_dim
+        self.config.vocab_size = vocab_size
+        self.config.encoder_num_layers = num_encoder_layers
+
+        self.conv1 = nn.Conv1d(mel_dim, hidden_dim, kernel_size=3, padding=1)
+        self.conv2 = nn.Conv1d(hidden_dim, hidden_dim, kernel_size=3, stride=2, padding=1)
+        self.encoder_layers = nn.ModuleList(
+            [DecoderLayer(hidden_dim, num_heads, self.head_dim, is_decoder=False) for _ in range(num_encoder_layers)])
+        self.encoder_norm = nn.LayerNorm(hidden_dim)
+        self.decoder_embed = nn.Embedding(vocab_size, hidden_dim)
+        self.decoder_layers = nn.ModuleList(
+            [DecoderLayer(hidden_dim, num_heads, self.head_dim, is_decoder=True) for _ in range(num_decoder_layers)])
+        self.decoder_norm = nn.LayerNorm(hidden_dim)
+        self.lm_head = nn.Linear(hidden_dim, vocab_size, bias=False)
+
+    # -- initialisation used by the benchmark configs ------------------------------
+    @torch.no_grad()
+    def init_normal_(self, std: float = 0.02, seed: int = 0) -> "WhisperClassSpeechEncoderDecoderModel":
+        """Weights of every Linear / Conv1d / Embedding ~ N(0, std) (seeded, drawn on
+        the CPU so any device gets the same values); biases 0; LayerNorm 1 / 0."""
+        g = torch.Generator().manual_seed(seed)
+        for m in self.modules():
+            if isinstance(m, (nn.Linear, nn.Conv1d, nn.Embedding)):
+                w = torch.empty(m.weight.shape, dtype=torch.float32).normal_(0.0, std, generator=g)
+                m.weight.copy_(w.to(m.weight.dtype))
+                if getattr(m, "bias", None) is not None:
+                    m.bias.zero_()
+            elif isinstance(m, nn.LayerNorm):
+                m.weight.fill_(1.0)
+                m.bias.zero_()
+        return self
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.decoder_norm.weight.dtype
+
+    def _embed(self, ids: torch.Tensor) -> torch.Tensor:
+        return self.decoder_embed(ids).to(dtype=self.decoder_norm.weight.dtype)
+
+    # -- encoder (models.py:349-367) ---------------------------------------------------
+    def encode(self, mel_features: torch.Tensor):
+        x = F.gelu(self.conv1(mel_features))
+        x = F.gelu(self.conv2(x)).transpose(1, 2)
+        kv = []
+        for layer in self.encoder_layers:
+            x, (k, v), _ = layer(x)
+            kv.append((k, v))
+        return self.encoder_norm(x), kv
+
+    def project_cross_kv(self, encoder_hidden_states: torch.Tensor) -> List[Tuple[torch.Tensor, torch.Tensor]]:
+        """Per decoder layer (K, V) [B, H, T, D] = cross_attn_k/v(encoder states) (models.py:179-181)."""
+        b, t, _ = encoder_hidden_states.shape
+        out = []
+        for layer in self.decoder_layers:
+            k = layer.cross_attn_k(encoder_hidden_states).view(b, t, self.num_heads, self.head_dim)
+            v = layer.cross_attn_v(encoder_hidden_states).view(b, t, self.num_heads, self.head_dim)
+            out.append((k.transpose(1, 2).contiguous(), v.transpose(1, 2).contiguous()))
+        return out
+
+    # -- paged decode (the hot path) -------------------------------------------------
+    def decode_step_paged(self, input_ids: torch.Tensor, kv: PagedKV, cross: Optional[CrossKV] = None,
+                          last_only: bool = True) -> torch.Tensor:
+        """Run the decoder on input_ids [B, Q] whose K/V go into the paged pool at
+        positions ctx_lens-Q .. ctx_lens-1; returns logits [B, V] of the last
+        position (or [B, Q, V])."""
+        x = self._embed(input_ids)
+        for l, layer in enumerate(self.decoder_layers):
+            x = layer.forward_paged(x, l, kv, cross)
+        x = self.decoder_norm(x[:, -1] if last_only else x)
+        return self.lm_head(x)
+
+    # -- contiguous decode, reference signature (models.py:369-423) --------------------
+    def decode_step(self, input_ids: torch.Tensor, past_key_values: Optional[Any] = None,
+                    encoder_past_kv_list: Optional[List[Tuple[torch.Tensor, torch.Tensor]]] = None,
+                    encoder_hidden_states: Optional[torch.Tensor] = None,
+                    attention_mask: Optional[torch.Tensor] = None,
+                    encoder_attention_mask: Optional[torch.Tensor] = None,
+                    position_ids: Optional[torch.Tensor] = None, use_cache: bool = True, **kwargs) -> ModelOutput:
+        x = self._embed(input_ids)
+        cache = KVCache() if use_cache else None
+        for i, layer in enumerate(self.decoder_layers):
+            past = None
+            if past_key_values is not None:
+                if hasattr(past_key_values, "layers"):
+                    if i < len(past_key_values.layers):
+                        past = (past_key_values.layers[i].keys, past_key_values.layers[i].values)
+                elif isinstance(past_key_values, (list, tuple)) and i < len(past_key_values):
+                    past = past_key_values[i]
+            enc_kv = encoder_past_kv_list[i] if encoder_past_kv_list is not None and i < len(
+                encoder_past_kv_list) else None
+            x, new_kv, _ = layer(x, past_key_values=past,
+                                 encoder_hidden_states=encoder_hidden_states if enc_kv is None else None,
+                                 encoder_past_kv=enc_kv, attention_mask=attention_mask,
+                                 encoder_attention_mask=encoder_attention_mask)
+            if use_cache:
+                cache.layers.append(LayerKV(new_kv[0], new_kv[1]))
+        return ModelOutput(self.lm_head(self.decoder_norm(x)), cache)
+
+    # -- bucketed static-KV decode, reference signature (models.py:425-487) -------------
+    def decode_step_graph_fixed(self, g_token_ids: torch.Tensor, g_positions: torch.Tensor, g_self_kv: torch.Tensor,
+                                g_cross_kv: torch.Tensor, g_output_tokens: torch.Tensor, bucket: int,
+                                max_slots: int, g_attn_mask: Optional[torch.Tensor] = None,
+                                g_cross_mask: Optional[torch.Tensor] = None) -> None:
+        """One decode step over static per-slot buffers g_self_kv [S, L, 2, H, bucket, D]
+        and g_cross_kv [S, L, 2, H, T, D]; masks are additive with -10000 beyond each
+        slot's length (graph_decode_buffers.py:527-537). Writes argmax tokens."""
+        x = self._embed(g_token_ids)
+        dev = x.device
+        if g_attn_mask is not None:
+            self_lens = (g_attn_mask.reshape(max_slots, -1) > -1000).sum(-1).to(torch.int32)
+        else:
+            self_lens = torch.full((max_slots,), bucket, dtype=torch.int32, device=dev)
+        t_enc = g_cross_kv.shape[4]
+        if g_cross_mask is not None:
+            cross_lens = (g_cross_mask.reshape(max_slots, -1) > -1000).sum(-1).to(torch.int32)
+        else:
+            cross_lens = torch.full((max_slots,), t_enc, dtype=torch.int32, device=dev)
+        pos = g_positions.view(max_slots).clamp(0, bucket - 1)
+        hd = self.num_heads * self.head_dim
+        for l, layer in enumerate(self.decoder_layers):
+            q, k, v = layer._qkv(x)
+            idx = pos.view(max_slots, 1, 1, 1).expand(max_slots, layer.num_heads, 1, layer.head_dim)
+            g_self_kv[:, l, 0].scatter_(2, idx, k.transpose(1, 2))
+            g_self_kv[:, l, 1].scatter_(2, idx, v.transpose(1, 2))
+            a = native.dense_attention(q, g_self_kv[:, l, 0], g_self_kv[:, l, 1], self_lens, bucket, layer.scale)
+            x = x + layer.self_attn_out(a.view(max_slots, 1, hd))
+            c = native.dense_attention(layer._cross_q(x), g_cross_kv[:, l, 0], g_cross_kv[:, l, 1], cross_lens,
+                                       t_enc, layer.scale)
+            x = x + layer.cross_attn_out(c.view(max_slots, 1, hd))
+            x = layer._finish(x, True)
+        logits = self.lm_head(self.decoder_norm(x[:, -1, :]))
+        native.argmax(logits, out=g_output_tokens)

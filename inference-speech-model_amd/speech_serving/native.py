@@ -34,6 +34,7 @@ SIGNATURES = {
     "skv_append": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_p]),
     "skv_gather": (_c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                             _c_i32, _c_i32, _c_p]),
+    "skv_argmax": (_c_int, [_c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p]),
     "skv_attention_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "skv_default_chunk_tokens": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "skv_paged_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p,
@@ -240,6 +241,36 @@ def gather(k_pool: torch.Tensor, v_pool: Optional[torch.Tensor], block_tables: t
                           _code(k_pool.dtype), _stream(k_pool.device))
     _check(rc, "skv_gather")
     return k_out, v_out
+
+
+def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, row_slots: Optional[torch.Tensor] = None,
+           slot_tokens: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Greedy tokens: first index of each row's maximum, int64 [rows].
+
+    logits: [rows, vocab] (row stride may exceed vocab). With row_slots
+    (int32 [rows]) and slot_tokens (int64), also slot_tokens[row_slots[r]] =
+    token for rows whose slot is >= 0. torch.argmax(dim=-1) semantics
+    (speech_serving/models.py:486-487).
+    """
+    _gpu(logits, "logits")
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise RuntimeError("argmax: logits must be [rows, vocab] with a contiguous last dim")
+    rows, vocab = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    if out.dtype != torch.int64 or out.numel() < rows or not out.is_contiguous():
+        raise RuntimeError("argmax: out must be contiguous int64 covering the rows")
+    if (row_slots is None) != (slot_tokens is None):
+        raise RuntimeError("argmax: row_slots and slot_tokens must both be given or both be None")
+    if row_slots is not None:
+        row_slots = _i32(row_slots, "row_slots")
+        _gpu(slot_tokens, "slot_tokens")
+        if slot_tokens.dtype != torch.int64 or not slot_tokens.is_contiguous() or row_slots.numel() < rows:
+            raise RuntimeError("argmax: slot_tokens must be contiguous int64 and row_slots must cover the rows")
+    rc = lib().skv_argmax(logits.data_ptr(), logits.stride(0), rows, vocab, _code(logits.dtype), out.data_ptr(),
+                          _ptr(row_slots), _ptr(slot_tokens), _stream(logits.device))
+    _check(rc, "skv_argmax")
+    return out
 
 
 def _q4(q: torch.Tensor, name: str) -> torch.Tensor:

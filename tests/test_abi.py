@@ -104,6 +104,14 @@ def test_attention_rejects_bad_group():
     assert rc == -1
 
 
+def test_argmax_rejects_bad_arguments():
+    lib = native.lib()
+    assert lib.skv_argmax(FAKE, 100, 4, 100, 9, FAKE, None, None, None) == -2
+    assert lib.skv_argmax(FAKE, 50, 4, 100, native.SKV_F16, FAKE, None, None, None) == -1  # stride < vocab
+    assert lib.skv_argmax(FAKE, 100, 4, 100, native.SKV_F16, FAKE, FAKE, None, None) == -1  # half the pair
+    assert lib.skv_argmax(FAKE, 100, 0, 100, native.SKV_F16, FAKE, None, None, None) == 0  # nothing to do
+
+
 def test_python_wrapper_refuses_cpu_tensors():
     import torch
 

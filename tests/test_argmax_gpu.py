@@ -1,0 +1,64 @@
+"""skv_argmax: greedy sampling with first-max tie-breaking and slot feedback.
+
+Integer results: must equal numpy's argmax (first occurrence) bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+from speech_serving import native
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("vocab", [1, 100, 51865, 51866])
+def test_argmax_matches_numpy_first_max(cuda, dtype, vocab):
+    gen = torch.Generator().manual_seed(vocab)
+    rows = 7
+    x = torch.randn(rows, vocab, generator=gen).to(dtype)
+    if vocab > 10:
+        x[1, 5] = x[1, vocab - 3] = 1e4  # tie: the first index wins
+        x[2, :] = -float("inf")           # all -inf: index 0
+        x[3, vocab // 2] = float("nan")    # NaN counts as the maximum
+        x[4, 7] = float("nan")
+        x[4, 3] = float("nan")             # first NaN wins
+    got = native.argmax(x.to(cuda)).cpu().numpy()
+    xf = x.float().numpy()
+    want = []
+    for r in range(rows):
+        nan = np.flatnonzero(np.isnan(xf[r]))
+        want.append(int(nan[0]) if nan.size else int(np.argmax(xf[r])))
+    assert got.tolist() == want
+    if vocab > 10:
+        assert got[1] == 5 and got[2] == 0 and got[3] == vocab // 2 and got[4] == 3
+
+
+def test_argmax_strided_rows_and_slot_feedback(cuda):
+    gen = torch.Generator().manual_seed(0)
+    full = torch.randn(5, 1, 300, generator=gen).to(cuda, torch.bfloat16)
+    logits = full[:, -1, :256]  # row stride 300, vocab 256
+    slots = torch.tensor([3, -1, 0, 7, 2], dtype=torch.int32, device=cuda)
+    slot_tokens = torch.full((9,), -5, dtype=torch.int64, device=cuda)
+    out = native.argmax(logits, row_slots=slots, slot_tokens=slot_tokens)
+    want = logits.float().cpu().numpy().argmax(axis=1)
+    assert out.cpu().tolist() == want.tolist()
+    st = slot_tokens.cpu().tolist()
+    assert st[3] == want[0] and st[0] == want[2] and st[7] == want[3] and st[2] == want[4]
+    assert st[1] == st[4] == st[5] == st[6] == st[8] == -5
+
+
+def test_argmax_in_graph_replays(cuda):
+    x = torch.zeros(4, 51866, dtype=torch.float16, device=cuda)
+    out = torch.zeros(4, dtype=torch.int64, device=cuda)
+    native.argmax(x, out=out)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        native.argmax(x, out=out)
+    for it in range(3):
+        gen = torch.Generator().manual_seed(it)
+        x.copy_(torch.randn(4, 51866, generator=gen).to(cuda, torch.float16))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert out.cpu().tolist() == x.float().cpu().numpy().argmax(axis=1).tolist()
