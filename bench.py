@@ -1,19 +1,26 @@
 """Benchmark of the decoder KV-cache hot path on one MI355X.
 
-Workload (default): paged decode attention for one decoder layer, fp16,
-32 heads x 64, block size 16, batch 64, per-sequence context U[1, 448], block
-tables a seeded random permutation of a 4096-block pool, Q/K/V ~ N(0, 1).
-One step = one fused launch that appends the batch's new token K/V into the
-pool through each sequence's block table and attends over the sequence's
-context (new token included). Inputs are resident in HBM before timing. Steps rotate over
-independent pool/table sets whose combined footprint exceeds the 256 MB
-last-level cache, so every step streams its K/V from HBM.
+Main workload (the JSON line's value): paged decode attention for one decoder
+layer, fp16, 32 heads x 64, block size 16, batch 64, per-sequence context
+U[1, 448], block tables a seeded random permutation of a 4096-block pool,
+Q/K/V ~ N(0, 1). One step = one fused launch that appends the batch's new
+token K/V into the pool through each sequence's block table and attends over
+the sequence's context (new token included). Inputs are resident in HBM
+before timing. Steps rotate over independent pool/table sets whose combined
+footprint exceeds the 256 MB last-level cache, so every step streams its K/V
+from HBM.
 
-Prints one JSON line: value = whole-step algorithmic HBM throughput (GB/s);
-`roofline` = the attention kernel alone (HIP events around each launch on
-its stream); `cpu_baseline` = the numpy oracle on a bounded sample.
+Extra fields (same JSON line), Whisper-large-v3 decoder shapes (bf16, 20 heads
+x 64, batch 64):
+  large_v3_paged_attention  the same fused kernel at ctx U[1, 452]
+  large_v3_cross_attention  attention over 1500 contiguous encoder positions
+  large_v3_decode           end-to-end greedy decode through the scheduler's
+                            captured graphs: 32 layers, d_model 1280, vocab
+                            51866, N(0, 0.02) weights, 64 requests x 448 tokens,
+                            random N(0,1) encoder states projected by cross_attn_k/v.
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline] [--no-large-v3]
+    python bench.py --mode copy    # known-size copy for PMC counter scaling
 """
 from __future__ import annotations
 
@@ -47,6 +54,10 @@ def parse():
     ap.add_argument("--chunk", type=int, default=0, help="split-K chunk (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-large-v3", action="store_true", help="skip the large-v3 kernel and decode measurements")
+    ap.add_argument("--decode-batch", type=int, default=64)
+    ap.add_argument("--decode-tokens", type=int, default=448)
+    ap.add_argument("--decode-layers", type=int, default=32)
     ap.add_argument("--mode", choices=["attention", "copy"], default="attention",
                     help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling")
     ap.add_argument("--copy-mib", type=int, default=512)
@@ -103,36 +114,55 @@ def append_bytes(batch, heads, d, elt):
 
 
 class ProblemSet:
-    """One independent copy of the workload: pool, tables, lengths, inputs."""
+    """One independent copy of a paged-attention workload: pool, tables, lengths, inputs."""
 
-    def __init__(self, torch, a, seed, device, dtype):
+    def __init__(self, torch, seed, device, dtype, batch, heads, d, bs, nb, max_ctx):
         g = torch.Generator().manual_seed(seed)
-        b, h, d, bs, nb = a.batch, a.heads, a.head_dim, a.block_size, a.pool_blocks
-        self.ctx = torch.randint(1, a.max_ctx + 1, (b,), generator=g)  # keys incl. the new token
-        maxblk = math.ceil(a.max_ctx / bs)
-        perm = torch.randperm(nb, generator=g)[: b * maxblk]
-        self.tables_cpu = perm.view(b, maxblk).to(torch.int32)
-        self.k_pool = torch.randn(nb, bs, h, d, generator=g).to(device, dtype)
-        self.v_pool = torch.randn(nb, bs, h, d, generator=g).to(device, dtype)
-        self.q = torch.randn(b, h, d, generator=g).to(device, dtype)
-        self.k_new = torch.randn(b, h, d, generator=g).to(device, dtype)
-        self.v_new = torch.randn(b, h, d, generator=g).to(device, dtype)
+        self.ctx = torch.randint(1, max_ctx + 1, (batch,), generator=g)  # keys incl. the new token
+        maxblk = math.ceil(max_ctx / bs)
+        perm = torch.randperm(nb, generator=g)[: batch * maxblk]
+        self.tables_cpu = perm.view(batch, maxblk).to(torch.int32)
+        self.k_pool = torch.randn(nb, bs, heads, d, generator=g).to(device, dtype)
+        self.v_pool = torch.randn(nb, bs, heads, d, generator=g).to(device, dtype)
+        self.q = torch.randn(batch, heads, d, generator=g).to(device, dtype)
+        self.k_new = torch.randn(batch, heads, d, generator=g).to(device, dtype)
+        self.v_new = torch.randn(batch, heads, d, generator=g).to(device, dtype)
         pos = (self.ctx - 1).tolist()
-        slots = [int(self.tables_cpu[i, p // bs]) * bs + p % bs for i, p in enumerate(pos)]
-        self.slots = torch.tensor(slots, dtype=torch.int64, device=device)
+        self.slots = [int(self.tables_cpu[i, p // bs]) * bs + p % bs for i, p in enumerate(pos)]
         self.tables = self.tables_cpu.to(device)
         self.ctx_dev = self.ctx.to(torch.int32).to(device)
         self.out = torch.empty_like(self.q)
+        elt = torch.empty((), dtype=dtype).element_size()
+        self.bytes = attention_bytes(self.ctx.tolist(), heads, d, elt, bs) + append_write_bytes(batch, heads, d, elt)
 
 
-def cpu_baseline(sets, a, scale, budget_s):
+def event_times_us(torch, fns, reps):
+    """HIP events around each launch on the current stream; first pass over fns is warm-up."""
+    cur = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i in range(reps):
+        evs[i][0].record(cur)
+        fns[i % len(fns)]()
+        evs[i][1].record(cur)
+    torch.cuda.synchronize()
+    return [evs[i][0].elapsed_time(evs[i][1]) * 1e3 for i in range(reps)]
+
+
+def paged_sets(torch, native, dev, dtype, batch, heads, d, bs, nb, max_ctx, seed, chunk):
+    one = ProblemSet(torch, seed, dev, dtype, batch, heads, d, bs, nb, max_ctx)
+    nsets = max(2, math.ceil(2 * LLC_BYTES / one.bytes) + 1)
+    sets = [one] + [ProblemSet(torch, seed + i, dev, dtype, batch, heads, d, bs, nb, max_ctx)
+                    for i in range(1, nsets)]
+    native.reserve_attention(batch, heads, d, max_ctx, dtype, dev, chunk)
+    return sets
+
+
+def cpu_baseline(s, a, scale, budget_s):
     """Time the numpy oracle (float64, one thread) on whole config batches."""
-    import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import paged_kv as O
 
-    s = sets[0]
     kp = s.k_pool.float().cpu().numpy()
     vp = s.v_pool.float().cpu().numpy()
     q = s.q.float().cpu().numpy()[:, None]
@@ -140,14 +170,13 @@ def cpu_baseline(sets, a, scale, budget_s):
     ctx = s.ctx.tolist()
     knew = s.k_new.float().cpu().numpy()
     vnew = s.v_new.float().cpu().numpy()
-    slots = s.slots.cpu().tolist()
     nbytes = attention_bytes(ctx, a.heads, a.head_dim, 2, a.block_size) + append_bytes(a.batch, a.heads,
                                                                                       a.head_dim, 2)
     passes = 0
     with threadpool_limits(limits=1):
         t0 = time.perf_counter()
         while True:
-            O.append(kp, vp, knew, vnew, slots)
+            O.append(kp, vp, knew, vnew, s.slots)
             O.paged_attention(q, kp, vp, tables, ctx, scale)
             passes += 1
             el = time.perf_counter() - t0
@@ -163,6 +192,90 @@ def cpu_baseline(sets, a, scale, budget_s):
                   f"{per * 1e3:.1f} ms per batch",
         "ms_per_step": round(per * 1e3, 3),
     }
+
+
+def large_v3_kernels(torch, native, dev, a):
+    """Fused paged attention and cross-attention at Whisper-large-v3 decoder shapes, batch 64, bf16."""
+    dt, b, h, d = torch.bfloat16, 64, 20, 64
+    out = {}
+    sets = paged_sets(torch, native, dev, dt, b, h, d, 16, 4096, 452, a.seed + 100, 0)
+    fns = [lambda s=s: native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, 0.125, out=s.out,
+                                              k_new=s.k_new, v_new=s.v_new) for s in sets]
+    durs = event_times_us(torch, fns, 10 * len(fns))[len(fns):]
+    avg = sum(durs) / len(durs)
+    byts = sum(s.bytes for s in sets) / len(sets)
+    out["large_v3_paged_attention"] = {
+        "shape": "bf16, 20 heads x 64, batch 64, block size 16, ctx U[1,452], fused append",
+        "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
+        "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1), "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del sets, fns
+    t = 1500
+    kvs = []
+    for i in range(2):  # 2 x 491 MB > 256 MB last-level cache
+        g = torch.Generator(device=dev).manual_seed(a.seed + 200 + i)
+        kvs.append((torch.randn(b, 2, h, t, d, generator=g, device=dev, dtype=dt),
+                    torch.randn(b, h, d, generator=g, device=dev, dtype=dt)))
+    lens = torch.full((b,), t, dtype=torch.int32, device=dev)
+    res = torch.empty(b, h, d, dtype=dt, device=dev)
+    native.reserve_attention(b, h, d, t, dt, dev)
+    fns = [lambda kv=kv: native.dense_attention(kv[1], kv[0][:, 0], kv[0][:, 1], lens, t, 0.125, out=res)
+           for kv in kvs]
+    durs = event_times_us(torch, fns, 20)[2:]
+    avg = sum(durs) / len(durs)
+    byts = b * (2 * t * h * d * 2 + 2 * h * d * 2 + 4)
+    out["large_v3_cross_attention"] = {
+        "shape": "bf16, 20 heads x 64, batch 64, 1500 encoder positions (g_cross_kv slot-major layer slice)",
+        "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
+        "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1), "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del kvs, fns
+    torch.cuda.empty_cache()
+    return out
+
+
+def large_v3_decode(torch, dev, a):
+    """Greedy decode of decode_batch requests x decode_tokens tokens through the scheduler's graphs."""
+    from speech_serving import (BlockManager, DualCacheManager, EncoderBlockManager, MemoryGuard,
+                                PhaseAwareSpeechScheduler, WhisperClassSpeechEncoderDecoderModel)
+    from speech_serving.phase_aware_scheduler import WHISPER_DEFAULT_PREFIX_TOKENS
+
+    dt, L, dm, h, vocab, t_enc, bs = torch.bfloat16, a.decode_layers, 1280, 20, 51866, 1500, 16
+    b, n = a.decode_batch, a.decode_tokens
+    model = WhisperClassSpeechEncoderDecoderModel(0, L, h, dm, 128, vocab, head_dim=64).to(dev, dt).eval()
+    model.init_normal_(0.02, seed=a.seed, draw_device=str(dev))
+    per_req = math.ceil((len(WHISPER_DEFAULT_PREFIX_TOKENS) + n) / bs)
+    dec = BlockManager(L, h, 64, bs, num_blocks=b * per_req + 8, dtype=dt, device=str(dev))
+    enc = EncoderBlockManager(1, h, 64, bs, num_blocks=8, dtype=dt, device=str(dev))
+    sched = PhaseAwareSpeechScheduler(model, DualCacheManager(enc, dec), MemoryGuard(high_water_mark_pct=101.0),
+                                      max_batch_size=b, device=str(dev), eos_token_id=-1, graph_decode=True,
+                                      graph_readback_k=4, graph_direct_encoder_kv=True, graph_max_enc_len=t_enc)
+    g = torch.Generator(device=dev).manual_seed(a.seed + 7)
+    with torch.no_grad():
+        for _ in range(b):
+            states = torch.randn(1, t_enc, dm, generator=g, device=dev, dtype=dt)
+            sched.submit_encoded(model.project_cross_kv(states),
+                                 prompt_token_ids=torch.tensor([WHISPER_DEFAULT_PREFIX_TOKENS]), max_new_tokens=n)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    done = sched.run_until_done()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    decode_tokens = sum(len(r.generated_tokens) - 1 for r in done)  # first token of each comes from prefill
+    ok = len(done) == b and all(len(r.generated_tokens) == n for r in done) and dec.allocated_block_count == 0
+    res = {
+        "workload": f"Whisper-large-v3-shaped greedy decode: {L} layers, d_model {dm}, {h} heads x 64, vocab "
+                    f"{vocab}, bf16 N(0,0.02) weights, {b} requests x {n} tokens from the 4-token prompt, "
+                    f"{t_enc} N(0,1) encoder positions projected by cross_attn_k/v, block size {bs}, "
+                    f"graph decode (batch bucket {b}, readback every 4 steps)",
+        "decode_tokens_per_s": round(decode_tokens / sched.decode_time_s, 1),
+        "ms_per_decode_step": round(sched.decode_time_s / max(sched.decode_steps, 1) * 1e3, 3),
+        "decode_steps": sched.decode_steps,
+        "decode_tokens": decode_tokens,
+        "wall_s_incl_prefill": round(wall, 3),
+        "completed_ok": ok,
+    }
+    del sched, model, dec, enc
+    torch.cuda.empty_cache()
+    return res
 
 
 def main():
@@ -182,16 +295,12 @@ def main():
         return
     dev = torch.device("cuda", 0)
     dtype = torch.float16
-    elt = 2
     scale = 1.0 / math.sqrt(a.head_dim)
     native.lib()
 
-    # Enough independent sets that consecutive reuse exceeds the last-level cache twice over.
-    one = ProblemSet(torch, a, a.seed, dev, dtype)
-    touched = attention_bytes(one.ctx.tolist(), a.heads, a.head_dim, elt, a.block_size)
-    nsets = max(2, math.ceil(2 * LLC_BYTES / touched) + 1)
-    sets = [one] + [ProblemSet(torch, a, a.seed + i, dev, dtype) for i in range(1, nsets)]
-    native.reserve_attention(a.batch, a.heads, a.head_dim, a.max_ctx, dtype, dev, a.chunk)
+    sets = paged_sets(torch, native, dev, dtype, a.batch, a.heads, a.head_dim, a.block_size, a.pool_blocks,
+                      a.max_ctx, a.seed, a.chunk)
+    nsets = len(sets)
 
     def step(s):
         native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, a.max_ctx, scale, out=s.out,
@@ -221,28 +330,13 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / a.steps * 1e3
+    value = sum(sets[i % nsets].bytes for i in range(a.steps)) / wall / 1e9
 
-    step_bytes = [attention_bytes(s.ctx.tolist(), a.heads, a.head_dim, elt, a.block_size) +
-                  append_write_bytes(a.batch, a.heads, a.head_dim, elt) for s in sets]
-    total_bytes = sum(step_bytes[i % nsets] for i in range(a.steps))
-    value = total_bytes / wall / 1e9
-
-    # Roofline of the dominant (and only) kernel: HIP events around each launch
-    # on the stream it runs on.
-    cur = torch.cuda.current_stream()
+    # Roofline of the dominant (and only) kernel: HIP events around each launch on its stream.
     n_ev = max(60, 3 * nsets)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
-    attn_bytes = step_bytes
-    for i in range(n_ev):
-        s = sets[i % nsets]
-        evs[i][0].record(cur)
-        step(s)
-        evs[i][1].record(cur)
-    torch.cuda.synchronize()
-    durs_us = [evs[i][0].elapsed_time(evs[i][1]) * 1e3 for i in range(n_ev)]
-    skip = nsets  # first pass over the sets is warm-up
-    avg_us = sum(durs_us[skip:]) / (n_ev - skip)
-    avg_bytes = sum(attn_bytes[i % nsets] for i in range(skip, n_ev)) / (n_ev - skip)
+    durs = event_times_us(torch, [lambda s=s: step(s) for s in sets], n_ev)[nsets:]
+    avg_us = sum(durs) / len(durs)
+    avg_bytes = sum(sets[i % nsets].bytes for i in range(nsets, n_ev)) / (n_ev - nsets)
     achieved = avg_bytes / (avg_us * 1e-6) / 1e9
 
     # Correctness guard on the measured data: one set against the oracle.
@@ -290,7 +384,8 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(a),
-            "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE per launch, scaled by a known-size copy (profiles/paged_attention_config2.md)",
+            "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE per launch, scaled by a known-size copy "
+                              "(profiles/paged_attention_config2.md)",
             "kernel": "attention_kernel<fp16, D=64, paged> with fused append",
             "avg_launch_us": round(avg_us, 3),
             "algorithmic_bytes_per_launch": int(avg_bytes),
@@ -298,7 +393,12 @@ def main():
         "max_abs_err_vs_oracle": max_err,
     }
     if not a.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(sets, a, scale, a.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(sets[0], a, scale, a.cpu_seconds)
+    del sets, graphs
+    torch.cuda.empty_cache()
+    if not a.no_large_v3:
+        result.update(large_v3_kernels(torch, native, dev, a))
+        result["large_v3_decode"] = large_v3_decode(torch, dev, a)
     print(json.dumps(result), flush=True)
 
 

@@ -307,13 +307,16 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
 
     # -- initialisation used by the benchmark configs ------------------------------
     @torch.no_grad()
-    def init_normal_(self, std: float = 0.02, seed: int = 0) -> "WhisperClassSpeechEncoderDecoderModel":
-        """Weights of every Linear / Conv1d / Embedding ~ N(0, std) (seeded, drawn on
-        the CPU so any device gets the same values); biases 0; LayerNorm 1 / 0."""
-        g = torch.Generator().manual_seed(seed)
+    def init_normal_(self, std: float = 0.02, seed: int = 0,
+                     draw_device: Optional[str] = None) -> "WhisperClassSpeechEncoderDecoderModel":
+        """Weights of every Linear / Conv1d / Embedding ~ N(0, std), biases 0,
+        LayerNorm 1 / 0. Draws are seeded on `draw_device` (default CPU, so every
+        device gets the same values; a GPU draw is much faster for large models)."""
+        dev = torch.device(draw_device or "cpu")
+        g = torch.Generator(device=dev).manual_seed(seed)
         for m in self.modules():
             if isinstance(m, (nn.Linear, nn.Conv1d, nn.Embedding)):
-                w = torch.empty(m.weight.shape, dtype=torch.float32).normal_(0.0, std, generator=g)
+                w = torch.empty(m.weight.shape, dtype=torch.float32, device=dev).normal_(0.0, std, generator=g)
                 m.weight.copy_(w.to(m.weight.dtype))
                 if getattr(m, "bias", None) is not None:
                     m.bias.zero_()
