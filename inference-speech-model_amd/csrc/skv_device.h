@@ -114,25 +114,56 @@ template <> __device__ __forceinline__ uint4 pack16<SKV_BF16>(const float* a) {
   return r;
 }
 
-// Lane exchange across the 64-lane wave. Offsets 1 and 2 use DPP quad
-// permutes; larger offsets use ds_swizzle/bpermute through __shfl_xor.
+__device__ __forceinline__ int lane_id() {
+  return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+// DPP controls (gfx9 encoding) used below; each reads lane f(i) into lane i.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]: i ^ 1
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]: i ^ 2
+constexpr int kDppXor3 = 0x1B;        // quad_perm [3,2,1,0]: i ^ 3
+constexpr int kDppHalfMirror = 0x141; // i ^ 7 (mirror of each 8-lane half row)
+constexpr int kDppRowMirror = 0x140;  // i ^ 15 (mirror of each 16-lane row)
+
+template <int CTRL> __device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Value of lane (lane ^ OFF), all in VALU and with every lane active (a DPP
+// read of a lane that is switched off returns the reader's own value, so no
+// lane-dependent branch may surround these): DPP within 16-lane rows, where
+// i^4 = (i^3)^7 and i^8 = (i^7)^15 compose two permutes; the gfx950
+// permlane16/32 swaps across rows. A swap of a register with itself returns
+// {even-half copy, odd-half copy} of the 16/32 split, so the partner's value
+// is picked by the lane's OFF bit with a select.
 template <int OFF> __device__ __forceinline__ float xor_lane(float x) {
   if constexpr (OFF == 1) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+    return dpp<kDppXor1>(x);
   } else if constexpr (OFF == 2) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
+    return dpp<kDppXor2>(x);
+  } else if constexpr (OFF == 4) {
+    return dpp<kDppXor3>(dpp<kDppHalfMirror>(x));
+  } else if constexpr (OFF == 8) {
+    return dpp<kDppHalfMirror>(dpp<kDppRowMirror>(x));
+  } else if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((lane_id() & 16) ? r[0] : r[1]);
   } else {
-    return __shfl_xor(x, OFF, 64);
+    static_assert(OFF == 32, "xor_lane: offset must be a power of two below 64");
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((lane_id() & 32) ? r[0] : r[1]);
   }
 }
 
 // Sum over groups of W adjacent lanes (W a power of two <= 64); every lane of
-// a group ends with the group's sum.
+// a group ends with the same bits. After the quad steps all lanes of a quad
+// (then of an 8-lane half row) hold one value, so the mirrors pair each lane
+// with a lane of the other half: one DPP op per step.
 template <int W> __device__ __forceinline__ float group_sum(float x) {
   if constexpr (W >= 2) x += xor_lane<1>(x);
   if constexpr (W >= 4) x += xor_lane<2>(x);
-  if constexpr (W >= 8) x += xor_lane<4>(x);
-  if constexpr (W >= 16) x += xor_lane<8>(x);
+  if constexpr (W >= 8) x += dpp<kDppHalfMirror>(x);
+  if constexpr (W >= 16) x += dpp<kDppRowMirror>(x);
   if constexpr (W >= 32) x += xor_lane<16>(x);
   if constexpr (W >= 64) x += xor_lane<32>(x);
   return x;

@@ -211,7 +211,12 @@ struct AttnParams {
   int32_t tstride;
   const int32_t* trows;
   int32_t bs, nb;
+  int32_t bs_shift;  // log2(bs) when bs is a power of two, else -1
   int64_t row_vecs;  // vectors per pool token row = Hkv * D / EPL
+  // Byte size of each of the K and V regions the kernel may read: the pools
+  // (paged) or one (slot, head) span of max_len keys (contiguous); the buffer
+  // fast path needs it below kBufLimit.
+  int64_t kv_bytes;
   // fused append (paged only): the Q newest keys of row b come from kn/vn
   // [B, Q, Hkv, D] and are written into the pool through the row's table.
   const uint4* kn;
@@ -227,9 +232,16 @@ struct AttnParams {
   float* part;  // [rows*heads*nchunk_max][D + kPartPad]
 };
 
+#ifndef SKV_ATTN_UNROLL
+#define SKV_ATTN_UNROLL 8  // most key rows a lane group loads before its math
+#endif
+#ifndef SKV_ATTN_SUB
+#define SKV_ATTN_SUB 64  // most keys one wave loads per loop trip
+#endif
 template <int TPI>
 constexpr int unroll_for() {
-  return (64 / TPI) < 1 ? 1 : ((64 / TPI) > 8 ? 8 : (64 / TPI));
+  return (SKV_ATTN_SUB / TPI) < 1 ? 1
+         : ((SKV_ATTN_SUB / TPI) > SKV_ATTN_UNROLL ? SKV_ATTN_UNROLL : (SKV_ATTN_SUB / TPI));
 }
 
 // Keys visible to query qi of batch row b.
@@ -240,18 +252,36 @@ __device__ __forceinline__ int visible_len(const AttnParams& p, int b, int qi) {
   return len > p.max_len ? p.max_len : len;
 }
 
-// Merge (m, l, acc) across the TPI lane groups of the wave (lane offsets
-// LPT, 2*LPT, ..., 32).
+// Merge the (m, l, acc) states of the TPI lane groups of a wave (lane offsets
+// LPT, 2*LPT, ..., 32): the common maximum first, then plain sums of the
+// rescaled l and acc. Every lane ends with the merged state of its dims.
+template <int OFF>
+__device__ __forceinline__ void max_steps(float& m) {
+  if constexpr (OFF < 64) {
+    m = fmaxf(m, xor_lane<OFF>(m));
+    max_steps<OFF * 2>(m);
+  }
+}
+template <int OFF, int N>
+__device__ __forceinline__ void sum_steps(float& l, float* acc) {
+  if constexpr (OFF < 64) {
+    l += xor_lane<OFF>(l);
+#pragma unroll
+    for (int e = 0; e < N; ++e) acc[e] += xor_lane<OFF>(acc[e]);
+    sum_steps<OFF * 2, N>(l, acc);
+  }
+}
 template <int LPT, int EPL>
 __device__ __forceinline__ void merge_groups(float& m, float& l, float* acc) {
+  if constexpr (LPT < 64) {
+    float mm = m;
+    max_steps<LPT>(mm);
+    const float s = __builtin_amdgcn_exp2f(m - (mm == kNegInf ? 0.f : mm));
+    l *= s;
 #pragma unroll
-  for (int off = LPT; off < 64; off <<= 1) {
-    const float m2 = __shfl_xor(m, off, 64);
-    const float l2 = __shfl_xor(l, off, 64);
-    float a2[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) a2[e] = __shfl_xor(acc[e], off, 64);
-    merge_state<EPL>(m, l, acc, m2, l2, a2);
+    for (int e = 0; e < EPL; ++e) acc[e] *= s;
+    sum_steps<LPT, EPL>(l, acc);
+    m = mm;
   }
 }
 
@@ -265,7 +295,55 @@ __device__ __forceinline__ void write_out(const AttnParams& p, int64_t o_off, fl
   p.o[o_off] = pack16<DT>(r);
 }
 
-template <int DT, int D, bool PAGED>
+// 16 zero bytes: the load target of key slots that hold no key (past the
+// row's length or behind an invalid block id), so every load is issued
+// unconditionally and an empty slot contributes an exact zero.
+__device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
+
+// One online-softmax step over N keys per lane group: scores from q.k (lane
+// group sum), masked by ok, then the rescale and the p*v accumulation.
+template <int DT, int LPT, int EPL, int N>
+__device__ __forceinline__ void softmax_step(const uint4& qv, const uint4* kr, const uint4* vr, const bool* ok,
+                                             float scale_log2, float& m, float& l, float* acc) {
+  float sc[N];
+  float mx = m;
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const float d = group_sum<LPT>(dot16<DT>(qv, kr[u]));
+    sc[u] = ok[u] ? d * scale_log2 : kNegInf;
+    mx = fmaxf(mx, sc[u]);
+  }
+  const float ref = (mx == kNegInf) ? 0.f : mx;
+  const float alpha = __builtin_amdgcn_exp2f(m - ref);
+  l *= alpha;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const float pr = __builtin_amdgcn_exp2f(sc[u] - ref);
+    l += pr;
+    axpy16<DT>(pr, vr[u], acc);
+  }
+  m = mx;
+}
+
+// Buffer fast path: K/V are read with buffer loads against a descriptor of
+// kv_bytes; an empty key slot gets an offset past that range, for which the
+// hardware returns zeros, so loads need no data select and offsets are 32-bit.
+constexpr int64_t kBufLimit = 0x7fffffff;
+constexpr uint32_t kBufOutOfRange = 0x80000000u;
+constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit dword format
+constexpr int kBufNt = 2;              // aux: nontemporal (keys are read once)
+
+__device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufNt);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Grid: x = query row * heads + head, y = key chunk. FAST: the buffer path;
+// for paged K/V it also needs a power-of-two block size (p.bs_shift), so
+// key -> (block, offset) is a shift and a mask.
+template <int DT, int D, bool PAGED, bool FAST>
 __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
   constexpr int EPL = Elt<DT>::EPL;
   constexpr int LPT = D / EPL;
@@ -280,19 +358,37 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int32_t rows = p.batch * p.qlen;
-  const int64_t per_chunk = (int64_t)rows * p.heads;
-  const int chunk = (int)(blockIdx.x / per_chunk);
-  if (chunk >= p.nchunk_max) return;
-  const int64_t rh = blockIdx.x - (int64_t)chunk * per_chunk;  // row * heads + head
-  const int row = (int)(rh / p.heads);
-  const int h = (int)(rh - (int64_t)row * p.heads);
+  const int chunk = blockIdx.y;
+  const int rh = blockIdx.x;  // row * heads + head
+  const int row = rh / p.heads;
+  const int h = rh - row * p.heads;
   const int b = row / p.qlen;
   const int qi = row - b * p.qlen;
-  const int len = visible_len(p, b, qi);
   const int g = lane / LPT;
   const int j = lane - g * LPT;
   const int64_t o_off = (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh + j;
+  const int t_begin = chunk * p.chunk;
+  const int kvh = h / p.group;
+  const uint4* zero = reinterpret_cast<const uint4*>(g_zero16);
+
+  // The row length, q and the chunk's block ids are independent loads: all
+  // are issued before any of them is waited on. Block ids are staged for the
+  // chunk's span up to max_len (inside the table row, which covers max_len),
+  // so the staging does not wait for the row length.
+  const int len = visible_len(p, b, qi);
+  const uint4 qv = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + j];
+  int first_blk = 0;
+  if constexpr (PAGED) {
+    const int trow = p.trows ? p.trows[b] : b;
+    const int32_t* tbl = p.tables + (int64_t)trow * p.tstride;
+    const int span_end = min(t_begin + p.chunk, p.max_len);
+    first_blk = t_begin / p.bs;
+    const int nblk = span_end > t_begin ? (span_end - 1) / p.bs - first_blk + 1 : 0;
+    for (int i = threadIdx.x; i < nblk; i += 64 * kWaves) {
+      const int blk = tbl[first_blk + i];
+      s_blk[i] = ((uint32_t)blk < (uint32_t)p.nb) ? blk : -1;
+    }
+  }
 
   if (len == 0) {
     if (chunk == 0 && wave == 0 && g == 0) p.o[o_off] = make_uint4(0u, 0u, 0u, 0u);
@@ -300,28 +396,19 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
   }
   const int nchunks = (len + p.chunk - 1) / p.chunk;
   if (chunk >= nchunks) return;  // uniform over the workgroup
-  const int t_begin = chunk * p.chunk;
   const int t_end = min(t_begin + p.chunk, len);
-  const int kvh = h / p.group;
 
+  // Keys [t_begin, pool_end) are read from K/V; with a fused append the
+  // newest keys [new_begin, len) come from kn/vn instead (fresh loop below).
+  int pool_end = t_end;
+  int new_begin = t_end;
   int64_t base = 0;
-  int first_blk = 0;
-  int new_begin = 0x7fffffff;  // keys at positions >= new_begin come from kn/vn
-  int64_t nbase = 0;
   if constexpr (PAGED) {
-    const int trow = p.trows ? p.trows[b] : b;
-    const int32_t* tbl = p.tables + (int64_t)trow * p.tstride;
-    first_blk = t_begin / p.bs;
-    const int nblk = (t_end - 1) / p.bs - first_blk + 1;
-    for (int i = threadIdx.x; i < nblk; i += 64 * kWaves) {
-      const int blk = tbl[first_blk + i];
-      s_blk[i] = ((uint32_t)blk < (uint32_t)p.nb) ? blk : -1;
-    }
     __syncthreads();
     base = (int64_t)kvh * LPT + j;
     if (p.kn) {
       new_begin = visible_len(p, b, p.qlen - 1) - p.qlen;
-      nbase = (int64_t)b * p.nsb - (int64_t)new_begin * p.nsq + (int64_t)kvh * p.nsh + j;
+      pool_end = max(t_begin, min(new_begin, t_end));
       // Append: the last query row's workgroups of the first head of each KV
       // group write the new keys of their chunk into the pool.
       if (qi == p.qlen - 1 && h % p.group == 0) {
@@ -348,63 +435,98 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
     base = (int64_t)slot * p.ss + (int64_t)kvh * p.sh + j;
   }
 
-  const uint4 qv = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + j];
-
   float m = kNegInf, l = 0.f;
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
 
-  for (int s = t_begin + wave * SUB; s < t_end; s += kWaves * SUB) {
-    uint4 kr[U], vr[U];
-    bool ok[U];
-    const uint4* kp[U];
-    const uint4* vp[U];
+  if constexpr (FAST) {
+    // 32-bit byte offsets against per-launch (paged) or per-workgroup (contiguous) descriptors.
+    const char* kb = reinterpret_cast<const char*>(p.k);
+    const char* vb = reinterpret_cast<const char*>(p.v);
+    if constexpr (!PAGED) {  // descriptor base: the workgroup's (slot, head) span
+      kb += (base - j) * 16;
+      vb += (base - j) * 16;
+    }
+    const __amdgpu_buffer_rsrc_t kres = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb), (short)0,
+                                                                          (int)p.kv_bytes, kBufWord3);
+    const __amdgpu_buffer_rsrc_t vres = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb), (short)0,
+                                                                          (int)p.kv_bytes, kBufWord3);
+    const uint32_t row_bytes = PAGED ? (uint32_t)p.row_vecs * 16u : (uint32_t)p.st * 16u;
+    const uint32_t col_bytes = PAGED ? (uint32_t)base * 16u : (uint32_t)j * 16u;
+    for (int s = t_begin + wave * SUB; s < pool_end; s += kWaves * SUB) {
+      uint32_t off[U];
+      bool ok[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = s + u * TPI + g;
-      bool valid = t < t_end;
-      if constexpr (PAGED) {
-        const int bi = t / p.bs;
-        const int blk = valid ? s_blk[min(bi - first_blk, kMaxChunkBlocks - 1)] : -1;
-        valid = blk >= 0;
-        const int64_t off = ((int64_t)blk * p.bs + (t - bi * p.bs)) * p.row_vecs + base;
-        const int64_t noff = nbase + (int64_t)t * p.nsq;
-        const bool fresh = t >= new_begin;
-        kp[u] = fresh ? p.kn + noff : p.k + off;
-        vp[u] = fresh ? p.vn + noff : p.v + off;
-      } else {
-        const int64_t off = base + (int64_t)t * p.st;
-        kp[u] = p.k + off;
-        vp[u] = p.v + off;
+      for (int u = 0; u < U; ++u) {
+        const int t = s + u * TPI + g;
+        bool valid = t < pool_end;
+        uint32_t row = (uint32_t)t;
+        if constexpr (PAGED) {
+          const int bi = t >> p.bs_shift;
+          const int blk = s_blk[min(bi - first_blk, kMaxChunkBlocks - 1)];
+          valid = valid && blk >= 0;
+          row = ((uint32_t)blk << p.bs_shift) | (uint32_t)(t & (p.bs - 1));
+        }
+        off[u] = valid ? row * row_bytes + col_bytes : kBufOutOfRange;
+        ok[u] = valid;
       }
-      ok[u] = valid;
-    }
+      uint4 kr[U], vr[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      kr[u] = ok[u] ? load_stream(kp[u]) : make_uint4(0u, 0u, 0u, 0u);
-      vr[u] = ok[u] ? load_stream(vp[u]) : make_uint4(0u, 0u, 0u, 0u);
-    }
-    float sc[U];
-    float mx = m;
+      for (int u = 0; u < U; ++u) kr[u] = load_buf(kres, off[u]);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float d = group_sum<LPT>(dot16<DT>(qv, kr[u]));
-      sc[u] = ok[u] ? d * p.scale_log2 : kNegInf;
-      mx = fmaxf(mx, sc[u]);
+      for (int u = 0; u < U; ++u) vr[u] = load_buf(vres, off[u]);
+      // Keep all 2*U loads in flight before the math: without this fence the
+      // scheduler may sink loads into the math to save registers, which
+      // serialises the memory latency.
+      __builtin_amdgcn_sched_barrier(0);
+      softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
     }
-    const float ref = (mx == kNegInf) ? 0.f : mx;
-    const float alpha = __builtin_amdgcn_exp2f(m - ref);
-    l *= alpha;
+  } else {
+    for (int s = t_begin + wave * SUB; s < pool_end; s += kWaves * SUB) {
+      const uint4* kp[U];
+      const uint4* vp[U];
+      bool ok[U];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
+      for (int u = 0; u < U; ++u) {
+        const int t = s + u * TPI + g;
+        bool valid = t < pool_end;
+        int64_t off;
+        if constexpr (PAGED) {
+          const int bi = t / p.bs;
+          const int blk = s_blk[min(bi - first_blk, kMaxChunkBlocks - 1)];
+          valid = valid && blk >= 0;
+          off = ((int64_t)blk * p.bs + (t - bi * p.bs)) * p.row_vecs + base;
+        } else {
+          off = base + (int64_t)t * p.st;
+        }
+        kp[u] = valid ? p.k + off : zero;
+        vp[u] = valid ? p.v + off : zero;
+        ok[u] = valid;
+      }
+      uint4 kr[U], vr[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float pr = __builtin_amdgcn_exp2f(sc[u] - ref);
-      l += pr;
-      axpy16<DT>(pr, vr[u], acc);
+      for (int u = 0; u < U; ++u) kr[u] = load_stream(kp[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) vr[u] = load_stream(vp[u]);
+      __builtin_amdgcn_sched_barrier(0);
+      softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
     }
-    m = mx;
+  }
+
+  if constexpr (PAGED) {
+    // Fresh keys of a fused append: at most q_len of them, one per lane group.
+    if (new_begin < t_end) {
+      const int64_t nbase = (int64_t)b * p.nsb + (int64_t)kvh * p.nsh + j;
+      for (int s = max(t_begin, new_begin) + wave * TPI; s < t_end; s += kWaves * TPI) {
+        const int t = s + g;
+        bool ok[1] = {t < t_end};
+        const int64_t off = nbase + (int64_t)(t - new_begin) * p.nsq;
+        const uint4 kr[1] = {load_stream(ok[0] ? p.kn + off : zero)};
+        const uint4 vr[1] = {load_stream(ok[0] ? p.vn + off : zero)};
+        softmax_step<DT, LPT, EPL, 1>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
+      }
+    }
   }
 
   merge_groups<LPT, EPL>(m, l, acc);
@@ -431,7 +553,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
     write_out<DT>(p, o_off, L, A);
     return;
   }
-  float* rec = p.part + (rh * p.nchunk_max + chunk) * PSTRIDE;
+  float* rec = p.part + ((int64_t)rh * p.nchunk_max + chunk) * PSTRIDE;
   float4* dst = reinterpret_cast<float4*>(rec + kPartPad + j * EPL);
 #pragma unroll
   for (int e = 0; e < EPL; e += 4) dst[e / 4] = make_float4(A[e], A[e + 1], A[e + 2], A[e + 3]);
@@ -499,8 +621,8 @@ int sub_tokens(int32_t dtype, int32_t d) {
   const int lpt = d / epl;
   if (lpt <= 0) return 0;
   const int tpi = 64 / lpt;
-  int u = 64 / tpi;
-  u = u < 1 ? 1 : (u > 8 ? 8 : u);
+  int u = SKV_ATTN_SUB / tpi;
+  u = u < 1 ? 1 : (u > SKV_ATTN_UNROLL ? SKV_ATTN_UNROLL : u);
   return tpi * u;
 }
 
@@ -528,8 +650,13 @@ bool supported_d(int32_t d) { return d == 16 || d == 32 || d == 64 || d == 128; 
 template <int DT, int D, bool PAGED>
 void launch_attention(const AttnParams& p, hipStream_t stream) {
   const int64_t rh = (int64_t)p.batch * p.qlen * p.heads;
-  hipLaunchKernelGGL((attention_kernel<DT, D, PAGED>), dim3((uint32_t)(rh * p.nchunk_max)), dim3(64 * kWaves), 0,
-                     stream, p);
+  const dim3 grid((uint32_t)rh, (uint32_t)p.nchunk_max);
+  const bool fast = p.kv_bytes <= kBufLimit && (!PAGED || p.bs_shift >= 0);
+  if (fast) {
+    hipLaunchKernelGGL((attention_kernel<DT, D, PAGED, true>), grid, dim3(64 * kWaves), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((attention_kernel<DT, D, PAGED, false>), grid, dim3(64 * kWaves), 0, stream, p);
+  }
   if (p.nchunk_max > 1)
     hipLaunchKernelGGL((merge_kernel<DT, D>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, stream, p);
 }
@@ -571,6 +698,10 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
   const int sub = sub_tokens(dtype, d);
   if (chunk % sub != 0) return fail(SKV_EINVAL, "%s: chunk_tokens %d must be a multiple of %d", who, chunk, sub);
   const int32_t nchunk_max = max_len > 0 ? (int32_t)cdiv(max_len, chunk) : 1;
+  // Grid: x = rows * heads workgroups (work-items must stay below 2^32), y = chunks.
+  if ((int64_t)batch * q_len * heads * 64 * kWaves >= ((int64_t)1 << 32) || nchunk_max > 65535)
+    return fail(SKV_EINVAL, "%s: launch too large (rows*heads=%lld, chunks=%d)", who,
+                (long long)batch * q_len * heads, nchunk_max);
   const int64_t need = workspace_bytes((int64_t)batch * q_len, heads, d, nchunk_max);
   if (need > 0 && (!ws || ws_bytes < need || !aligned16(ws)))
     return fail(SKV_EWORKSPACE, "%s: workspace needs %lld bytes (16-byte aligned), got %lld", who, (long long)need,
@@ -742,8 +873,10 @@ int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   p.tstride = table_stride;
   p.trows = table_rows;
   p.bs = block_size;
+  p.bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
   p.nb = num_blocks;
   p.row_vecs = (int64_t)num_kv_heads * head_dim / (16 / elt_bytes(dtype));
+  p.kv_bytes = (int64_t)num_blocks * block_size * p.row_vecs * 16;
   rc = dispatch_attention<true>(dtype, head_dim, p, (hipStream_t)stream);
   if (rc != SKV_OK) return rc;
   return check_launch("skv_paged_attention");
@@ -767,6 +900,9 @@ int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   p.ss = kv_stride_s / epl;
   p.sh = kv_stride_h / epl;
   p.st = kv_stride_t / epl;
+  // One (slot, head) span: max_len keys at the key stride, plus one key row.
+  p.kv_bytes = max_len > 0 ? ((int64_t)(max_len - 1) * (p.st < 0 ? -p.st : p.st) + head_dim / epl) * 16 : 16;
+  if (p.st < 0) p.kv_bytes = kBufLimit + 1;  // negative key strides take the 64-bit path
   p.slots = slot_ids;
   rc = dispatch_attention<false>(dtype, head_dim, p, (hipStream_t)stream);
   if (rc != SKV_OK) return rc;
