@@ -114,11 +114,17 @@ def append_bytes(batch, heads, d, elt):
 
 
 class ProblemSet:
-    """One independent copy of a paged-attention workload: pool, tables, lengths, inputs."""
+    """One independent copy of a paged-attention workload: pool, tables, lengths, inputs.
 
-    def __init__(self, torch, seed, device, dtype, batch, heads, d, bs, nb, max_ctx):
+    Rows are laid out longest-first, as the engine lays out its decode batch
+    (sorted=False keeps the drawn order).
+    """
+
+    def __init__(self, torch, seed, device, dtype, batch, heads, d, bs, nb, max_ctx, sorted_rows=True):
         g = torch.Generator().manual_seed(seed)
         self.ctx = torch.randint(1, max_ctx + 1, (batch,), generator=g)  # keys incl. the new token
+        if sorted_rows:
+            self.ctx = self.ctx.sort(descending=True).values
         maxblk = math.ceil(max_ctx / bs)
         perm = torch.randperm(nb, generator=g)[: batch * maxblk]
         self.tables_cpu = perm.view(batch, maxblk).to(torch.int32)
@@ -136,22 +142,41 @@ class ProblemSet:
         self.bytes = attention_bytes(self.ctx.tolist(), heads, d, elt, bs) + append_write_bytes(batch, heads, d, elt)
 
 
-def event_times_us(torch, fns, reps):
-    """HIP events around each launch on the current stream; first pass over fns is warm-up."""
-    cur = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for i in range(reps):
-        evs[i][0].record(cur)
-        fns[i % len(fns)]()
-        evs[i][1].record(cur)
+def graph_launch_us(torch, fns, per_fn=8, replays=7):
+    """Average duration of one launch, from HIP events around replays of a captured graph that
+    holds per_fn back-to-back launches of every fn (rotating through fns). The events sit on the
+    stream the graph is replayed on; the gap between dependent launches is included."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    n = per_fn * len(fns)
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fns[i % len(fns)]()
+    g.replay()
     torch.cuda.synchronize()
-    return [evs[i][0].elapsed_time(evs[i][1]) * 1e3 for i in range(reps)]
+    cur = torch.cuda.current_stream()
+    per = []
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(cur)
+        g.replay()
+        b.record(cur)
+        b.synchronize()
+        per.append(a.elapsed_time(b) * 1e3 / n)
+    del g
+    per.sort()
+    return per[len(per) // 2]
 
 
-def paged_sets(torch, native, dev, dtype, batch, heads, d, bs, nb, max_ctx, seed, chunk):
-    one = ProblemSet(torch, seed, dev, dtype, batch, heads, d, bs, nb, max_ctx)
+def paged_sets(torch, native, dev, dtype, batch, heads, d, bs, nb, max_ctx, seed, chunk, sorted_rows=True):
+    one = ProblemSet(torch, seed, dev, dtype, batch, heads, d, bs, nb, max_ctx, sorted_rows)
     nsets = max(2, math.ceil(2 * LLC_BYTES / one.bytes) + 1)
-    sets = [one] + [ProblemSet(torch, seed + i, dev, dtype, batch, heads, d, bs, nb, max_ctx)
+    sets = [one] + [ProblemSet(torch, seed + i, dev, dtype, batch, heads, d, bs, nb, max_ctx, sorted_rows)
                     for i in range(1, nsets)]
     native.reserve_attention(batch, heads, d, max_ctx, dtype, dev, chunk)
     return sets
@@ -198,17 +223,25 @@ def large_v3_kernels(torch, native, dev, a):
     """Fused paged attention and cross-attention at Whisper-large-v3 decoder shapes, batch 64, bf16."""
     dt, b, h, d = torch.bfloat16, 64, 20, 64
     out = {}
-    sets = paged_sets(torch, native, dev, dt, b, h, d, 16, 4096, 452, a.seed + 100, 0)
-    fns = [lambda s=s: native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, 0.125, out=s.out,
-                                              k_new=s.k_new, v_new=s.v_new) for s in sets]
-    durs = event_times_us(torch, fns, 10 * len(fns))[len(fns):]
-    avg = sum(durs) / len(durs)
-    byts = sum(s.bytes for s in sets) / len(sets)
-    out["large_v3_paged_attention"] = {
-        "shape": "bf16, 20 heads x 64, batch 64, block size 16, ctx U[1,452], fused append",
-        "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
-        "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1), "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    del sets, fns
+    for sorted_rows in (True, False):
+        sets = paged_sets(torch, native, dev, dt, b, h, d, 16, 4096, 452, a.seed + 100, 0, sorted_rows)
+        fns = [lambda s=s: native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, 0.125,
+                                                  out=s.out, k_new=s.k_new, v_new=s.v_new) for s in sets]
+        avg = graph_launch_us(torch, fns)
+        byts = sum(s.bytes for s in sets) / len(sets)
+        if sorted_rows:
+            out["large_v3_paged_attention"] = {
+                "shape": "bf16, 20 heads x 64, batch 64, block size 16, ctx U[1,452], fused append, "
+                         "rows longest-first",
+                "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
+                "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1),
+                "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        else:
+            r = out["large_v3_paged_attention"]
+            r["unsorted_rows_avg_launch_us"] = round(avg, 3)
+            r["unsorted_rows_frac"] = round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        del sets, fns
+        torch.cuda.empty_cache()
     t = 1500
     kvs = []
     for i in range(2):  # 2 x 491 MB > 256 MB last-level cache
@@ -220,8 +253,7 @@ def large_v3_kernels(torch, native, dev, a):
     native.reserve_attention(b, h, d, t, dt, dev)
     fns = [lambda kv=kv: native.dense_attention(kv[1], kv[0][:, 0], kv[0][:, 1], lens, t, 0.125, out=res)
            for kv in kvs]
-    durs = event_times_us(torch, fns, 20)[2:]
-    avg = sum(durs) / len(durs)
+    avg = graph_launch_us(torch, fns, per_fn=4, replays=5)
     byts = b * (2 * t * h * d * 2 + 2 * h * d * 2 + 4)
     out["large_v3_cross_attention"] = {
         "shape": "bf16, 20 heads x 64, batch 64, 1500 encoder positions (g_cross_kv slot-major layer slice)",
@@ -332,11 +364,10 @@ def main():
     ms_per_step = wall / a.steps * 1e3
     value = sum(sets[i % nsets].bytes for i in range(a.steps)) / wall / 1e9
 
-    # Roofline of the dominant (and only) kernel: HIP events around each launch on its stream.
-    n_ev = max(60, 3 * nsets)
-    durs = event_times_us(torch, [lambda s=s: step(s) for s in sets], n_ev)[nsets:]
-    avg_us = sum(durs) / len(durs)
-    avg_bytes = sum(sets[i % nsets].bytes for i in range(nsets, n_ev)) / (n_ev - nsets)
+    # Roofline of the dominant (and only) kernel: HIP events around replays of a graph of
+    # back-to-back launches on the replay stream.
+    avg_us = graph_launch_us(torch, [lambda s=s: step(s) for s in sets])
+    avg_bytes = sum(s.bytes for s in sets) / nsets
     achieved = avg_bytes / (avg_us * 1e-6) / 1e9
 
     # Correctness guard on the measured data: one set against the oracle.
@@ -375,6 +406,7 @@ def main():
             "pool_blocks": a.pool_blocks,
             "max_ctx": a.max_ctx,
             "rotating_sets": nsets,
+            "rows": "longest-first (the engine's decode batch layout)",
             "chunk_tokens": a.chunk or native.default_chunk_tokens(a.batch, a.heads, a.head_dim, a.max_ctx, dtype),
         },
         "roofline": {
@@ -395,6 +427,15 @@ def main():
     if not a.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(sets[0], a, scale, a.cpu_seconds)
     del sets, graphs
+    torch.cuda.empty_cache()
+    # The same workload with the rows in drawn order, for comparison.
+    sets = paged_sets(torch, native, dev, dtype, a.batch, a.heads, a.head_dim, a.block_size, a.pool_blocks,
+                      a.max_ctx, a.seed, a.chunk, sorted_rows=False)
+    un_us = graph_launch_us(torch, [lambda s=s: step(s) for s in sets])
+    result["roofline"]["unsorted_rows_avg_launch_us"] = round(un_us, 3)
+    result["roofline"]["unsorted_rows_frac"] = round(sum(s.bytes for s in sets) / len(sets) / (un_us * 1e-6) / 1e9
+                                                     / HBM_PEAK_GBS, 4)
+    del sets
     torch.cuda.empty_cache()
     if not a.no_large_v3:
         result.update(large_v3_kernels(torch, native, dev, a))

@@ -278,7 +278,10 @@ class GraphDecodeBuffers:
 
     def prepare_replay(self) -> int:
         """Fill a pinned bank with the active slots' rows and upload it; returns the bucket."""
-        active = [s for s in self.slots if s.active]
+        # Rows longest-first: the attention workgroups of a launch then land on the
+        # compute units with long and short contexts mixed, which evens the
+        # per-unit load. The row -> slot map of every step is kept for readback.
+        active = sorted((s for s in self.slots if s.active), key=lambda s: -s.decoder_seq_len)
         bucket = self.pick_bucket(len(active))
         bank_idx = self._step_counter % self._n_banks
         if self._bank_in_flight[bank_idx]:

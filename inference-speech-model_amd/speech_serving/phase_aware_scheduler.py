@@ -511,7 +511,9 @@ class PhaseAwareSpeechScheduler:
         t0 = time.perf_counter()
         dec_bm = self.dual_cache.decoder_bm
         bs = dec_bm.block_size
-        reqs = self.active_decode
+        # Batch rows longest-first (evens the attention kernel's per-unit load);
+        # results go back to the requests, whose order is kept.
+        reqs = sorted(self.active_decode, key=lambda r: -r.decoder_seq_len)
         try:
             for r in reqs:  # block-boundary allocation (reference :780-783)
                 if r.decoder_seq_len % bs == 0:
@@ -549,8 +551,10 @@ class PhaseAwareSpeechScheduler:
                 self._complete_request(r, status=RequestPhase.FAILED)
             self.active_decode = []
             return
+        tok_of = {id(r): tok for r, tok in zip(reqs, toks)}
         still = []
-        for r, tok in zip(reqs, toks):
+        for r in self.active_decode:
+            tok = tok_of[id(r)]
             r.decoder_seq_len += 1
             r.last_token_id = tok
             r.generated_tokens.append(tok)
