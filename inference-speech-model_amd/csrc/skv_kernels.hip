@@ -57,6 +57,11 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Raw buffer descriptors (gfx9 word 3: 32-bit dword format) and the load
+// cache hint for data read once (nontemporal).
+constexpr int kBufWord3 = 0x00020000;
+constexpr int kBufNt = 2;
+
 // ---------------------------------------------------------------------------
 // Append: pool[slot] = new row, 16 bytes per thread, K in grid.y 0, V in 1.
 // ---------------------------------------------------------------------------
@@ -121,52 +126,82 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint4* __restrict__ k
 // Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
 // (NaN counts as the maximum, as in torch.argmax). Optionally also writes the
 // token to slot_tokens[row_slots[r]] (skipped when the slot is negative).
-// One 256-thread workgroup per row.
+// One 1024-thread workgroup per row reads the row as 32-bit words through a
+// buffer descriptor (past-the-end words read as zero and are not compared),
+// kArgmaxWords words per thread in flight; a 16-bit row that starts in the
+// middle of a word has its first element handled alone.
 // ---------------------------------------------------------------------------
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxWords = 32;  // words per thread per pass: 65536 16-bit logits in one pass
+
 __device__ __forceinline__ bool argmax_better(float v1, int i1, float v2, int i2) {
   const bool n1 = v1 != v1, n2 = v2 != v2;
   if (n1 || n2) return n1 && (!n2 || i1 < i2);
   return v1 > v2 || (v1 == v2 && i1 < i2);
 }
 
-template <int DT>
-__device__ __forceinline__ float load_logit(const void* row, int i);
-template <> __device__ __forceinline__ float load_logit<SKV_F32>(const void* row, int i) {
-  return ((const float*)row)[i];
+template <int DT> __device__ __forceinline__ float half_word(uint32_t w, int hi);
+template <> __device__ __forceinline__ float half_word<SKV_F16>(uint32_t w, int hi) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? w >> 16 : w & 0xffffu));
 }
-template <> __device__ __forceinline__ float load_logit<SKV_F16>(const void* row, int i) {
-  return (float)((const _Float16*)row)[i];
-}
-template <> __device__ __forceinline__ float load_logit<SKV_BF16>(const void* row, int i) {
-  return __uint_as_float((uint32_t)((const uint16_t*)row)[i] << 16);
+template <> __device__ __forceinline__ float half_word<SKV_BF16>(uint32_t w, int hi) {
+  return __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
 }
 
 template <int DT>
-__global__ __launch_bounds__(256) void argmax_kernel(const char* __restrict__ logits, int64_t row_bytes,
-                                                     int32_t vocab, int64_t* __restrict__ out,
-                                                     const int32_t* __restrict__ row_slots,
-                                                     int64_t* __restrict__ slot_tokens) {
-  __shared__ float s_v[4];
-  __shared__ int s_i[4];
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __restrict__ logits, int64_t row_bytes,
+                                                                int32_t vocab, int64_t* __restrict__ out,
+                                                                const int32_t* __restrict__ row_slots,
+                                                                int64_t* __restrict__ slot_tokens) {
+  __shared__ float s_v[kArgmaxThreads / 64];
+  __shared__ int s_i[kArgmaxThreads / 64];
   const int r = blockIdx.x;
   const char* row = logits + (int64_t)r * row_bytes;
   float best = kNegInf;
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < vocab; i += 256) {
-    const float v = load_logit<DT>(row, i);
+  auto consider = [&](float v, int i) {
     if (argmax_better(v, i, best, bi)) {
       best = v;
       bi = i;
+    }
+  };
+  // Elements per word, the element held alone before the first word, and the word count.
+  constexpr int EPW = DT == SKV_F32 ? 1 : 2;
+  const int head = (EPW == 2 && ((uintptr_t)row & 3u)) ? 1 : 0;
+  const char* words = row + head * 2;
+  const int nw = (vocab - head) / EPW;
+  const __amdgpu_buffer_rsrc_t res =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(words), (short)0, nw * 4, kBufWord3);
+  for (int w0 = threadIdx.x; w0 < nw; w0 += kArgmaxThreads * kArgmaxWords) {
+    uint32_t x[kArgmaxWords];
+#pragma unroll
+    for (int k = 0; k < kArgmaxWords; ++k)
+      x[k] = __builtin_amdgcn_raw_buffer_load_b32(res, (uint32_t)(w0 + k * kArgmaxThreads) * 4u, 0, kBufNt);
+#pragma unroll
+    for (int k = 0; k < kArgmaxWords; ++k) {
+      const int w = w0 + k * kArgmaxThreads;
+      if (w < nw) {
+        if constexpr (EPW == 1) {
+          consider(__uint_as_float(x[k]), w);
+        } else {
+          consider(half_word<DT>(x[k], 0), head + 2 * w);
+          consider(half_word<DT>(x[k], 1), head + 2 * w + 1);
+        }
+      }
+    }
+  }
+  if constexpr (EPW == 2) {
+    if (threadIdx.x == 0) {
+      const uint16_t* e = reinterpret_cast<const uint16_t*>(row);
+      if (head) consider(half_word<DT>(e[0], 0), 0);
+      if ((vocab - head) & 1) consider(half_word<DT>(e[vocab - 1], 0), vocab - 1);
     }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float v2 = __shfl_xor(best, off, 64);
     const int i2 = __shfl_xor(bi, off, 64);
-    if (argmax_better(v2, i2, best, bi)) {
-      best = v2;
-      bi = i2;
-    }
+    consider(v2, i2);
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
@@ -175,11 +210,7 @@ __global__ __launch_bounds__(256) void argmax_kernel(const char* __restrict__ lo
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w)
-      if (argmax_better(s_v[w], s_i[w], best, bi)) {
-        best = s_v[w];
-        bi = s_i[w];
-      }
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) consider(s_v[w], s_i[w]);
     const int64_t tok = bi == 0x7fffffff ? 0 : bi;
     out[r] = tok;
     if (row_slots) {
@@ -332,8 +363,6 @@ __device__ __forceinline__ void softmax_step(const uint4& qv, const uint4* kr, c
 // hardware returns zeros, so loads need no data select and offsets are 32-bit.
 constexpr int64_t kBufLimit = 0x7fffffff;
 constexpr uint32_t kBufOutOfRange = 0x80000000u;
-constexpr int kBufWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit dword format
-constexpr int kBufNt = 2;              // aux: nontemporal (keys are read once)
 
 __device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufNt);
@@ -799,7 +828,7 @@ int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t voc
                int64_t* out_tokens, const int32_t* row_slots, int64_t* slot_tokens, void* stream) {
   const int eb = elt_bytes(dtype);
   if (eb == 0) return fail(SKV_EDTYPE, "skv_argmax: unknown dtype %d", dtype);
-  if (rows < 0 || vocab <= 0 || row_stride < vocab)
+  if (rows < 0 || vocab <= 0 || vocab >= (1 << 29) || row_stride < vocab)
     return fail(SKV_EINVAL, "skv_argmax: bad sizes rows=%d vocab=%d row_stride=%lld", rows, vocab,
                 (long long)row_stride);
   if (rows == 0) return SKV_OK;
@@ -809,15 +838,15 @@ int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t voc
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case SKV_F32:
-      hipLaunchKernelGGL(argmax_kernel<SKV_F32>, dim3(rows), dim3(256), 0, s, (const char*)logits, rb, vocab,
+      hipLaunchKernelGGL(argmax_kernel<SKV_F32>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
                          out_tokens, row_slots, slot_tokens);
       break;
     case SKV_F16:
-      hipLaunchKernelGGL(argmax_kernel<SKV_F16>, dim3(rows), dim3(256), 0, s, (const char*)logits, rb, vocab,
+      hipLaunchKernelGGL(argmax_kernel<SKV_F16>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
                          out_tokens, row_slots, slot_tokens);
       break;
     default:
-      hipLaunchKernelGGL(argmax_kernel<SKV_BF16>, dim3(rows), dim3(256), 0, s, (const char*)logits, rb, vocab,
+      hipLaunchKernelGGL(argmax_kernel<SKV_BF16>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
                          out_tokens, row_slots, slot_tokens);
       break;
   }

@@ -62,3 +62,21 @@ def test_argmax_in_graph_replays(cuda):
         g.replay()
         torch.cuda.synchronize()
         assert out.cpu().tolist() == x.float().cpu().numpy().argmax(axis=1).tolist()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("vocab", [2, 3, 4097, 51865])
+def test_argmax_rows_starting_mid_word(cuda, dtype, vocab):
+    # A view one element into each row: every row starts 2 bytes past a 4-byte
+    # boundary, so the first element is read alone; odd lengths leave a last one.
+    gen = torch.Generator().manual_seed(vocab + 1)
+    full = torch.randn(6, vocab + 1, generator=gen).to(dtype)
+    full[0, 1] = 100.0          # the maximum is the first element of the view
+    full[1, vocab] = 100.0      # ... or its last element
+    full[2, 1 + vocab // 2] = 100.0
+    x = full.to(cuda)[:, 1:]
+    assert x.data_ptr() % 4 == 2
+    got = native.argmax(x).cpu().numpy()
+    want = x.float().cpu().numpy().argmax(axis=1)
+    assert got.tolist() == want.tolist()
+    assert got[0] == 0 and got[1] == vocab - 1
