@@ -21,14 +21,17 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include "skv_common.h"
 #include "skv_device.h"
 #include "speech_kv.h"
 
-using namespace skv;
+namespace skv {
 
 namespace {
-
 thread_local char g_last_error[512] = "";
+}  // namespace
+
+const char* last_error() { return g_last_error; }
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -53,14 +56,11 @@ int elt_bytes(int32_t dtype) {
   }
 }
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+}  // namespace skv
 
-inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+using namespace skv;
 
-// Raw buffer descriptors (gfx9 word 3: 32-bit dword format) and the load
-// cache hint for data read once (nontemporal).
-constexpr int kBufWord3 = 0x00020000;
-constexpr int kBufNt = 2;
+namespace {
 
 // ---------------------------------------------------------------------------
 // Append: pool[slot] = new row, 16 bytes per thread, K in grid.y 0, V in 1.
@@ -362,7 +362,6 @@ __device__ __forceinline__ void softmax_step(const uint4& qv, const uint4* kr, c
 // kv_bytes; an empty key slot gets an offset past that range, for which the
 // hardware returns zeros, so loads need no data select and offsets are 32-bit.
 constexpr int64_t kBufLimit = 0x7fffffff;
-constexpr uint32_t kBufOutOfRange = 0x80000000u;
 
 __device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kBufNt);
@@ -768,7 +767,7 @@ extern "C" {
 
 const char* skv_version(void) { return "speechkv 0.2.0 gfx950"; }
 
-const char* skv_last_error(void) { return g_last_error; }
+const char* skv_last_error(void) { return skv::last_error(); }
 
 int skv_append(const void* k_new, const void* v_new, int64_t new_stride_n, int64_t new_stride_h, void* k_pool,
                void* v_pool, const int64_t* slot_mapping, int32_t n_tokens, int32_t num_heads, int32_t head_dim,
