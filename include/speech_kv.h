@@ -197,6 +197,23 @@ SKV_API int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_str
                         int32_t dtype, int32_t chunk_tokens,
                         void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * skv_add_layernorm — residual add + LayerNorm of a decode batch.
+ *   x, y : [rows, hidden] at row strides ldx, ldy (y NULL: no add, sum unused)
+ *   sum  : x + y rounded to dtype (may be x itself; NULL: not stored)
+ *   norm : LayerNorm(sum) * gamma + beta, fp32 statistics with the population
+ *          variance and eps, as torch.nn.LayerNorm; gamma, beta [hidden].
+ *   hidden a multiple of the 16-byte vector (8 fp16/bf16, 4 fp32), at most 64*8
+ *   vectors; rows 16-byte aligned.
+ * Replaces the pre-LN residual step `x = x + f(x)` followed by `norm(x)` of the
+ * decoder layers, speech_serving/models.py:126-208 (norm1/norm2/norm3 and the
+ * final decoder norm), each pair in one launch.
+ */
+SKV_API int skv_add_layernorm(const void* x, int64_t ldx, const void* y, int64_t ldy,
+                              const void* gamma, const void* beta, float eps,
+                              void* sum, int64_t lds, void* norm, int64_t ldn,
+                              int32_t rows, int32_t hidden, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -221,6 +221,125 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
 }
 
 // ---------------------------------------------------------------------------
+// Residual add + LayerNorm of a decode batch (the pre-LN transformer's
+// `x = x + f(x); h = norm(x)`): sum = x + y rounded to the tensor type, as the
+// separate add would store it; norm = (sum - mean) / sqrt(var + eps) * gamma +
+// beta over the row with fp32 statistics (population variance, two passes over
+// registers), as torch.nn.LayerNorm computes it. One wave per row holds the row
+// in registers: VPL 16-byte vectors per lane.
+// ---------------------------------------------------------------------------
+template <int DT> __device__ __forceinline__ void unpack16(const uint4& v, float* f);
+template <> __device__ __forceinline__ void unpack16<SKV_F32>(const uint4& v, float* f) {
+  f[0] = __uint_as_float(v.x), f[1] = __uint_as_float(v.y), f[2] = __uint_as_float(v.z), f[3] = __uint_as_float(v.w);
+}
+template <> __device__ __forceinline__ void unpack16<SKV_F16>(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const half2v h = __builtin_bit_cast(half2v, w[i]);
+    f[2 * i] = (float)h.x;
+    f[2 * i + 1] = (float)h.y;
+  }
+}
+template <> __device__ __forceinline__ void unpack16<SKV_BF16>(const uint4& v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_lo(w[i]);
+    f[2 * i + 1] = bf16_hi(w[i]);
+  }
+}
+
+struct AddNormParams {
+  const uint4* x;
+  const uint4* y;  // NULL: no add
+  const uint4* gamma;
+  const uint4* beta;
+  uint4* sum;      // NULL: sum not stored
+  uint4* norm;
+  int64_t ldx, ldy, lds, ldn;  // row strides in 16-byte vectors
+  int32_t rows, vecs;          // vectors per row
+  float eps, inv_n;
+};
+
+template <int DT, int VPL>
+__global__ __launch_bounds__(256) void add_layernorm_kernel(AddNormParams p) {
+  constexpr int EPL = Elt<DT>::EPL;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;  // uniform over the wave
+  float v[VPL][EPL];
+  uint4 raw[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c = lane + 64 * j;
+    raw[j] = c < p.vecs ? p.x[row * p.ldx + c] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  if (p.y) {
+    uint4 ry[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const int c = lane + 64 * j;
+      ry[j] = c < p.vecs ? p.y[row * p.ldy + c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float a[EPL], b[EPL];
+      unpack16<DT>(raw[j], a);
+      unpack16<DT>(ry[j], b);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) a[e] += b[e];
+      raw[j] = pack16<DT>(a);  // rounded to the tensor type, like the stored sum
+      const int c = lane + 64 * j;
+      if (p.sum && c < p.vecs) p.sum[row * p.lds + c] = raw[j];
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    unpack16<DT>(raw[j], v[j]);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) s += v[j][e];
+  }
+  const float mean = group_sum<64>(s) * p.inv_n;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    if (lane + 64 * j < p.vecs) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const float d = v[j][e] - mean;
+        q = fmaf(d, d, q);
+      }
+    }
+  }
+  const float rstd = rsqrtf(group_sum<64>(q) * p.inv_n + p.eps);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c >= p.vecs) continue;
+    float g[EPL], b[EPL], o[EPL];
+    unpack16<DT>(p.gamma[c], g);
+    unpack16<DT>(p.beta[c], b);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) o[e] = (v[j][e] - mean) * rstd * g[e] + b[e];
+    p.norm[row * p.ldn + c] = pack16<DT>(o);
+  }
+}
+
+template <int DT>
+void launch_add_layernorm(const AddNormParams& p, int vpl, hipStream_t s) {
+  const dim3 grid((uint32_t)cdiv(p.rows, 4));
+  switch (vpl) {
+    case 1: hipLaunchKernelGGL((add_layernorm_kernel<DT, 1>), grid, dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((add_layernorm_kernel<DT, 2>), grid, dim3(256), 0, s, p); break;
+    case 3: hipLaunchKernelGGL((add_layernorm_kernel<DT, 3>), grid, dim3(256), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((add_layernorm_kernel<DT, 4>), grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL((add_layernorm_kernel<DT, 8>), grid, dim3(256), 0, s, p); break;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Attention.
 // ---------------------------------------------------------------------------
 #ifndef SKV_ATTN_WAVES
@@ -850,6 +969,46 @@ int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t voc
       break;
   }
   return check_launch("skv_argmax");
+}
+
+int skv_add_layernorm(const void* x, int64_t ldx, const void* y, int64_t ldy, const void* gamma, const void* beta,
+                      float eps, void* sum, int64_t lds, void* norm, int64_t ldn, int32_t rows, int32_t hidden,
+                      int32_t dtype, void* stream) {
+  const int eb = elt_bytes(dtype);
+  if (eb == 0) return fail(SKV_EDTYPE, "skv_add_layernorm: unknown dtype %d", dtype);
+  const int epl = 16 / eb;
+  if (rows < 0 || hidden <= 0 || hidden % epl || hidden > 64 * 8 * epl)
+    return fail(SKV_EINVAL, "skv_add_layernorm: hidden %d must be a multiple of %d and at most %d (rows=%d)", hidden,
+                epl, 64 * 8 * epl, rows);
+  if (rows == 0) return SKV_OK;
+  if (!x || !gamma || !beta || !norm) return fail(SKV_EINVAL, "skv_add_layernorm: null pointer argument");
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(beta) || !aligned16(norm) || (y && !aligned16(y)) ||
+      (sum && !aligned16(sum)) || ldx % epl || ldy % epl || lds % epl || ldn % epl)
+    return fail(SKV_EALIGN, "skv_add_layernorm: rows must be 16-byte aligned");
+  if (!(eps >= 0.f)) return fail(SKV_EINVAL, "skv_add_layernorm: eps must be >= 0");
+  AddNormParams p{};
+  p.x = (const uint4*)x;
+  p.y = (const uint4*)y;
+  p.gamma = (const uint4*)gamma;
+  p.beta = (const uint4*)beta;
+  p.sum = y ? (uint4*)sum : nullptr;
+  p.norm = (uint4*)norm;
+  p.ldx = ldx / epl;
+  p.ldy = ldy / epl;
+  p.lds = lds / epl;
+  p.ldn = ldn / epl;
+  p.rows = rows;
+  p.vecs = hidden / epl;
+  p.eps = eps;
+  p.inv_n = 1.f / (float)hidden;
+  const int vpl = (int)cdiv(p.vecs, 64);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case SKV_F32: launch_add_layernorm<SKV_F32>(p, vpl, s); break;
+    case SKV_F16: launch_add_layernorm<SKV_F16>(p, vpl, s); break;
+    default: launch_add_layernorm<SKV_BF16>(p, vpl, s); break;
+  }
+  return check_launch("skv_add_layernorm");
 }
 
 int64_t skv_attention_workspace_bytes(int32_t rows, int32_t num_heads, int32_t head_dim, int32_t max_len,

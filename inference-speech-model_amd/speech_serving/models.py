@@ -138,6 +138,16 @@ def _compact(k: torch.Tensor, v: torch.Tensor, keep: torch.Tensor):
     return torch.gather(k, 2, idx).contiguous(), torch.gather(v, 2, idx).contiguous(), lens
 
 
+def add_norm(x: torch.Tensor, y: Optional[torch.Tensor], norm: nn.LayerNorm) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(s, norm(s)) for s = x + y (s = x when y is None): one skv_add_layernorm launch
+    on the GPU, the same two torch ops elsewhere."""
+    if x.is_cuda and norm.elementwise_affine and norm.bias is not None and \
+            native.add_layernorm_supported(x, norm.weight):
+        return native.add_layernorm(x, y, norm.weight, norm.bias, norm.eps)
+    s = x if y is None else x + y
+    return s, norm(s)
+
+
 # ---------------------------------------------------------------------------
 # Layers.
 # ---------------------------------------------------------------------------
@@ -183,9 +193,13 @@ class DecoderLayer(nn.Module):
         return self._qkv_w
 
     def _qkv(self, x: torch.Tensor):
-        b, s, _ = x.shape
+        return self._qkv_normed(self.norm1(x))
+
+    def _qkv_normed(self, h: torch.Tensor):
+        """q, k, v [B, S, H, D] from the already normalised input h."""
+        b, s, _ = h.shape
         hd = self.num_heads * self.head_dim
-        qkv = F.linear(self.norm1(x), self.qkv_weight())
+        qkv = F.linear(h, self.qkv_weight())
         shape = (b, s, self.num_heads, self.head_dim)
         return qkv[..., :hd].view(shape), qkv[..., hd:2 * hd].view(shape), qkv[..., 2 * hd:].view(shape)
 
@@ -198,20 +212,30 @@ class DecoderLayer(nn.Module):
         return self.cross_attn_q(self.norm2(x)).view(b, s, self.num_heads, self.head_dim)
 
     # -- paged hot path ---------------------------------------------------------
-    def forward_paged(self, x: torch.Tensor, layer: int, kv: PagedKV, cross: Optional[CrossKV]) -> torch.Tensor:
+    def forward_paged(self, x: torch.Tensor, layer: int, kv: PagedKV, cross: Optional[CrossKV],
+                      pending: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        """One decoder layer over the paged cache. The residual stream is x + pending
+        (pending: the previous layer's MLP output, not yet added). Returns (x, mlp
+        output) with the MLP output left for the next layer (or the final norm) to
+        add, so every residual add shares a launch with the LayerNorm that follows it."""
         b, s, _ = x.shape
         hd = self.num_heads * self.head_dim
-        q, k, v = self._qkv(x)
+        x, h = add_norm(x, pending, self.norm1)
+        q, k, v = self._qkv_normed(h)
         attn = native.paged_attention(q, kv.k_pools[layer], kv.v_pools[layer], kv.block_tables, kv.ctx_lens,
                                       kv.max_ctx, self.scale, causal=s > 1, table_rows=kv.table_rows,
                                       k_new=k, v_new=v)
-        x = x + self.self_attn_out(attn.view(b, s, hd))
+        a = self.self_attn_out(attn.view(b, s, hd))
         used = cross is not None and cross.has(layer)
         if used:
-            c = native.dense_attention(self._cross_q(x), cross.k[layer], cross.v[layer], cross.lens,
+            x, h = add_norm(x, a, self.norm2)
+            cq = self.cross_attn_q(h).view(b, s, self.num_heads, self.head_dim)
+            c = native.dense_attention(cq, cross.k[layer], cross.v[layer], cross.lens,
                                        cross.max_len, self.scale, slot_ids=cross.slot_ids)
-            x = x + self.cross_attn_out(c.view(b, s, hd))
-        return self._finish(x, used)
+            x, h = add_norm(x, self.cross_attn_out(c.view(b, s, hd)), self.norm3)
+        else:
+            x, h = add_norm(x, a, self.norm2)
+        return x, self.mlp(h)
 
     # -- contiguous API of the reference (models.py:110-208) ---------------------
     def forward(self, x: torch.Tensor, past_key_values: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
@@ -359,10 +383,14 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
         positions ctx_lens-Q .. ctx_lens-1; returns logits [B, V] of the last
         position (or [B, Q, V])."""
         x = self._embed(input_ids)
+        pending = None
         for l, layer in enumerate(self.decoder_layers):
-            x = layer.forward_paged(x, l, kv, cross)
-        x = self.decoder_norm(x[:, -1] if last_only else x)
-        return self.lm_head(x)
+            x, pending = layer.forward_paged(x, l, kv, cross, pending)
+        if last_only:
+            x = x[:, -1]
+            pending = None if pending is None else pending[:, -1]
+        _, h = add_norm(x, pending, self.decoder_norm)
+        return self.lm_head(h)
 
     # -- contiguous decode, reference signature (models.py:369-423) --------------------
     def decode_step(self, input_ids: torch.Tensor, past_key_values: Optional[Any] = None,

@@ -44,6 +44,8 @@ SIGNATURES = {
     "skv_dense_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p,
                                      _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                      _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p]),
+    "skv_add_layernorm": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_f, _c_p, _c_i64, _c_p, _c_i64,
+                                   _c_i32, _c_i32, _c_i32, _c_p]),
 }
 
 
@@ -402,3 +404,52 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: tor
         1 if causal else 0, _code(q4.dtype), chunk_tokens, wp, wn, _stream(q.device))
     _check(rc, "skv_dense_attention")
     return out
+
+
+def add_layernorm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether skv_add_layernorm takes this LayerNorm: a GPU tensor of a supported dtype whose
+    hidden size is a multiple of the 16-byte vector (and at most 512 vectors), with 16-byte rows."""
+    if not x.is_cuda or x.dtype not in _DTYPE_CODE or weight.dtype != x.dtype:
+        return False
+    h = x.shape[-1]
+    epl = 16 // x.element_size()
+    if h % epl or h > 512 * epl or x.stride(-1) != 1:
+        return False
+    rows = x.numel() // h if h else 0
+    x2 = x.reshape(rows, h) if rows else x
+    return rows == 0 or (x2.stride(0) % epl == 0 and x2.data_ptr() % 16 == 0)
+
+
+def add_layernorm(x: torch.Tensor, y: Optional[torch.Tensor], weight: torch.Tensor, bias: torch.Tensor,
+                  eps: float, sum_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(s, LayerNorm(s)) with s = x + y rounded to x's dtype (s = x when y is None).
+
+    x, y [..., hidden]; weight, bias [hidden]. sum_out may be x (in-place residual).
+    """
+    _gpu(x, "x")
+    h = x.shape[-1]
+    if not add_layernorm_supported(x, weight):
+        raise RuntimeError("add_layernorm: unsupported dtype/hidden size/layout")
+    rows = x.numel() // h
+    x2 = x.reshape(rows, h)
+    y2 = None
+    if y is not None:
+        _gpu(y, "y")
+        y2 = y.reshape(rows, h)
+        if y2.dtype != x.dtype or y2.stride(-1) != 1 or y2.data_ptr() % 16:
+            raise RuntimeError("add_layernorm: y must match x's dtype with 16-byte rows")
+        if sum_out is None:
+            sum_out = torch.empty_like(x)
+    s2 = sum_out.reshape(rows, h) if sum_out is not None else None
+    norm = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    n2 = norm.view(rows, h)
+    for t, name in ((weight, "weight"), (bias, "bias")):
+        if not t.is_contiguous() or t.numel() != h or t.dtype != x.dtype:
+            raise RuntimeError(f"add_layernorm: {name} must be contiguous [hidden] in x's dtype")
+    ld = lambda t: t.stride(0) if rows > 1 else h  # noqa: E731
+    rc = lib().skv_add_layernorm(x2.data_ptr(), ld(x2), _ptr(y2), ld(y2) if y2 is not None else h,
+                                 weight.data_ptr(), bias.data_ptr(), float(eps),
+                                 _ptr(s2), ld(s2) if s2 is not None else h, n2.data_ptr(), h, rows, h,
+                                 _code(x.dtype), _stream(x.device))
+    _check(rc, "skv_add_layernorm")
+    return (sum_out if y is not None else x), norm

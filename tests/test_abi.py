@@ -112,6 +112,21 @@ def test_argmax_rejects_bad_arguments():
     assert lib.skv_argmax(FAKE, 100, 0, 100, native.SKV_F16, FAKE, None, None, None) == 0  # nothing to do
 
 
+def test_add_layernorm_rejects_bad_arguments():
+    lib = native.lib()
+
+    def call(dtype=native.SKV_BF16, hidden=1280, ldx=1280, rows=4, eps=1e-5):
+        return lib.skv_add_layernorm(FAKE, ldx, None, hidden, FAKE, FAKE, eps, None, hidden, FAKE, hidden, rows,
+                                     hidden, dtype, None)
+
+    assert call(dtype=7) == -2
+    assert call(hidden=1284, ldx=1288) == -1      # not a multiple of 8 bf16 elements
+    assert call(hidden=8192, ldx=8192) == -1      # more than 512 vectors per row
+    assert call(ldx=1284) == -3                   # row stride breaks 16-byte alignment
+    assert call(eps=-1.0) == -1
+    assert call(rows=0) == 0
+
+
 def test_python_wrapper_refuses_cpu_tensors():
     import torch
 
