@@ -269,11 +269,15 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(AddNormParams p) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= p.rows) return;  // uniform over the wave
   float v[VPL][EPL];
-  uint4 raw[VPL];
+  uint4 raw[VPL], gv[VPL], bv[VPL];
+  // Every load up front (x, y, gamma, beta): one memory round trip per row.
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int c = lane + 64 * j;
-    raw[j] = c < p.vecs ? p.x[row * p.ldx + c] : make_uint4(0u, 0u, 0u, 0u);
+    const bool in = c < p.vecs;
+    raw[j] = in ? p.x[row * p.ldx + c] : make_uint4(0u, 0u, 0u, 0u);
+    gv[j] = in ? p.gamma[c] : make_uint4(0u, 0u, 0u, 0u);
+    bv[j] = in ? p.beta[c] : make_uint4(0u, 0u, 0u, 0u);
   }
   if (p.y) {
     uint4 ry[VPL];
@@ -319,8 +323,8 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(AddNormParams p) {
     const int c = lane + 64 * j;
     if (c >= p.vecs) continue;
     float g[EPL], b[EPL], o[EPL];
-    unpack16<DT>(p.gamma[c], g);
-    unpack16<DT>(p.beta[c], b);
+    unpack16<DT>(gv[j], g);
+    unpack16<DT>(bv[j], b);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) o[e] = (v[j][e] - mean) * rstd * g[e] + b[e];
     p.norm[row * p.ldn + c] = pack16<DT>(o);
