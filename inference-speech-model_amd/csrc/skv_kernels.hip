@@ -528,6 +528,17 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
   // so the staging does not wait for the row length.
   const int len = visible_len(p, b, qi);
   const uint4 qv = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + j];
+  // A fused append of one key (q_len 1, the decode step): the last wave loads
+  // the new K/V row here, with q, scores it before the pool loop and writes it
+  // to the pool from registers, so the append adds no memory round trip. Its
+  // kn/vn address does not depend on the row length.
+  const bool one_new = PAGED && p.kn && p.qlen == 1;
+  uint4 nk = make_uint4(0u, 0u, 0u, 0u), nv = nk;
+  if (one_new && wave == kWaves - 1 && g == 0) {
+    const int64_t noff = (int64_t)b * p.nsb + (int64_t)kvh * p.nsh + j;
+    nk = p.kn[noff];
+    nv = p.vn[noff];
+  }
   int first_blk = 0;
   if constexpr (PAGED) {
     const int trow = p.trows ? p.trows[b] : b;
@@ -554,12 +565,34 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
   int pool_end = t_end;
   int new_begin = t_end;
   int64_t base = 0;
+  float m = kNegInf, l = 0.f;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
   if constexpr (PAGED) {
     __syncthreads();
     base = (int64_t)kvh * LPT + j;
     if (p.kn) {
       new_begin = visible_len(p, b, p.qlen - 1) - p.qlen;
       pool_end = max(t_begin, min(new_begin, t_end));
+    }
+    if (one_new) {
+      // The new key is len - 1; the chunk that holds it (uniform test) scores it
+      // in the last wave, and the first head of each KV group stores it.
+      if (new_begin >= t_begin && new_begin < t_end && wave == kWaves - 1) {
+        const bool ok[1] = {g == 0};
+        softmax_step<DT, LPT, EPL, 1>(qv, &nk, &nv, ok, p.scale_log2, m, l, acc);
+        if (g == 0 && h % p.group == 0) {
+          const int bi = new_begin / p.bs;
+          const int blk = s_blk[bi - first_blk];
+          if (blk >= 0) {
+            const int64_t dst = ((int64_t)blk * p.bs + (new_begin - bi * p.bs)) * p.row_vecs + base;
+            const_cast<uint4*>(p.k)[dst] = nk;
+            const_cast<uint4*>(p.v)[dst] = nv;
+          }
+        }
+      }
+    } else if (p.kn) {
       // Append: the last query row's workgroups of the first head of each KV
       // group write the new keys of their chunk into the pool.
       if (qi == p.qlen - 1 && h % p.group == 0) {
@@ -585,11 +618,6 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
     const int slot = p.slots ? p.slots[b] : b;
     base = (int64_t)slot * p.ss + (int64_t)kvh * p.sh + j;
   }
-
-  float m = kNegInf, l = 0.f;
-  float acc[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
 
   if constexpr (FAST) {
     // 32-bit byte offsets against per-launch (paged) or per-workgroup (contiguous) descriptors.
@@ -666,8 +694,8 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
   }
 
   if constexpr (PAGED) {
-    // Fresh keys of a fused append: at most q_len of them, one per lane group.
-    if (new_begin < t_end) {
+    // Fresh keys of a fused append with q_len > 1: one per lane group.
+    if (!one_new && new_begin < t_end) {
       const int64_t nbase = (int64_t)b * p.nsb + (int64_t)kvh * p.nsh + j;
       for (int s = max(t_begin, new_begin) + wave * TPI; s < t_end; s += kWaves * TPI) {
         const int t = s + g;
