@@ -17,6 +17,8 @@
 //     boundary orders the two, so no device-scope fence runs inside a kernel.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -382,6 +384,14 @@ struct AttnParams {
   // common
   const int32_t* lens;
   int32_t batch, qlen, heads, group, max_len, causal, chunk, nchunk_max;
+  int32_t grid3d;  // grid (heads, rows, chunks) instead of (rows * heads, chunks)
+  // Snake order (one chunk, grid3d): workgroup w of the dispatch order runs on
+  // CU w mod 2^cu_shift while the grid fits one resident generation, so odd
+  // rounds of 2^cu_shift workgroups take the (row, head) items in reverse; with
+  // rows longest-first every CU then holds a mix of long and short rows.
+  // row = umulhi(item, heads_magic), exact for items * heads < 2^32.
+  int32_t snake, cu_shift;
+  uint32_t items, heads_magic;
   float scale_log2;
   float* part;  // [rows*heads*nchunk_max][D + kPartPad]
 };
@@ -509,24 +519,83 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int chunk = blockIdx.y;
-  const int rh = blockIdx.x;  // row * heads + head
-  const int row = rh / p.heads;
-  const int h = rh - row * p.heads;
-  const int b = row / p.qlen;
-  const int qi = row - b * p.qlen;
+  // Every parameter on the prologue's address chain, read in one scalar batch:
+  // left alone, the compiler spreads these reads over several waits, each a
+  // scalar memory round trip before the first K/V load can issue.
+  // The asm has no memory effects (so the loads behind it keep their scalar
+  // form) and its zero output feeds the workgroup index, which places it first.
+  uint32_t batch0;
+  asm("s_mov_b32 %0, 0"
+      : "=s"(batch0)
+      : "s"(p.lens), "s"(p.trows), "s"(p.tables), "s"(p.q), "s"(p.qsb), "s"(p.qsh), "s"(p.heads), "s"(p.qlen),
+        "s"(p.group), "s"(p.snake), "s"(p.cu_shift), "s"(p.items), "s"(p.heads_magic), "s"(p.grid3d),
+        "s"(p.tstride), "s"(p.chunk), "s"(p.max_len), "s"(p.causal), "s"(p.bs), "s"(p.nb));
+  uint32_t batch1;
+  asm("s_mov_b32 %0, 0"
+      : "=s"(batch1)
+      : "s"(p.qsq), "s"(p.o), "s"(p.osb), "s"(p.osq), "s"(p.osh), "s"(p.k), "s"(p.v), "s"(p.bs_shift),
+        "s"(p.row_vecs), "s"(p.kv_bytes), "s"(p.kn), "s"(p.vn), "s"(p.nsb), "s"(p.nsh), "s"(p.nchunk_max),
+        "s"(p.scale_log2));
+  const uint32_t bx = blockIdx.x + batch0 + batch1;
+  // Grid (heads, rows, chunks), or (rows * heads, chunks) when the rows exceed
+  // the y limit. Every wave of a CU's resident workgroups runs this prologue on
+  // the CU's one scalar unit before its first memory access, so the common
+  // shapes (q_len 1, no KV grouping, one chunk) take no integer division.
+  int h, row, chunk;
+  if (p.snake) {
+    const uint32_t w = bx + blockIdx.y * (uint32_t)p.heads;
+    const uint32_t round = (1u << p.cu_shift) - 1u;
+    const uint32_t base = w & ~round;
+    uint32_t item = w;
+    if ((w >> p.cu_shift) & 1u) {
+      const uint32_t n = min(round + 1u, p.items - base);
+      item = base + (n - 1u) - (w - base);
+    }
+    row = (int)__umulhi(item, p.heads_magic);
+    h = (int)item - row * p.heads;
+    chunk = 0;
+  } else if (p.grid3d) {
+    h = bx;
+    row = blockIdx.y;
+    chunk = blockIdx.z;
+  } else {
+    row = bx / p.heads;
+    h = bx - row * p.heads;
+    chunk = blockIdx.y;
+  }
+  const int rh = row * p.heads + h;
+  int b = row, qi = 0;
+  if (p.qlen != 1) {
+    b = row / p.qlen;
+    qi = row - b * p.qlen;
+  }
   const int g = lane / LPT;
   const int j = lane - g * LPT;
   const int64_t o_off = (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh + j;
   const int t_begin = chunk * p.chunk;
-  const int kvh = h / p.group;
+  const int kvh = p.group == 1 ? h : h / p.group;
   const uint4* zero = reinterpret_cast<const uint4*>(g_zero16);
 
-  // The row length, q and the chunk's block ids are independent loads: all
-  // are issued before any of them is waited on. Block ids are staged for the
-  // chunk's span up to max_len (inside the table row, which covers max_len),
-  // so the staging does not wait for the row length.
+  // Loads in the order of the address chain: the row length and the table row
+  // (scalar), then the chunk's block ids (the only load the workgroup barrier
+  // waits for), then q and the fused-append row, which are first needed after
+  // the first K/V loads have been issued. Block ids are staged for the chunk's
+  // span up to max_len (inside the table row, which covers max_len), so the
+  // staging does not wait for the row length.
   const int len = visible_len(p, b, qi);
+  int first_blk = 0;
+  if constexpr (PAGED) {
+    const int trow = p.trows ? p.trows[b] : b;
+    const int32_t* tbl = p.tables + (int64_t)trow * p.tstride;
+    const int span_end = min(t_begin + p.chunk, p.max_len);
+    first_blk = FAST ? t_begin >> p.bs_shift : t_begin / p.bs;
+    const int last_blk = FAST ? (span_end - 1) >> p.bs_shift : (span_end - 1) / p.bs;
+    const int nblk = span_end > t_begin ? last_blk - first_blk + 1 : 0;
+    for (int i = threadIdx.x; i < nblk; i += 64 * kWaves) {
+      const int blk = tbl[first_blk + i];
+      s_blk[i] = ((uint32_t)blk < (uint32_t)p.nb) ? blk : -1;
+    }
+  }
   const uint4 qv = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + j];
   // A fused append of one key (q_len 1, the decode step): the last wave loads
   // the new K/V row here, with q, scores it before the pool loop and writes it
@@ -539,24 +608,12 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
     nk = p.kn[noff];
     nv = p.vn[noff];
   }
-  int first_blk = 0;
-  if constexpr (PAGED) {
-    const int trow = p.trows ? p.trows[b] : b;
-    const int32_t* tbl = p.tables + (int64_t)trow * p.tstride;
-    const int span_end = min(t_begin + p.chunk, p.max_len);
-    first_blk = t_begin / p.bs;
-    const int nblk = span_end > t_begin ? (span_end - 1) / p.bs - first_blk + 1 : 0;
-    for (int i = threadIdx.x; i < nblk; i += 64 * kWaves) {
-      const int blk = tbl[first_blk + i];
-      s_blk[i] = ((uint32_t)blk < (uint32_t)p.nb) ? blk : -1;
-    }
-  }
 
   if (len == 0) {
     if (chunk == 0 && wave == 0 && g == 0) p.o[o_off] = make_uint4(0u, 0u, 0u, 0u);
     return;
   }
-  const int nchunks = (len + p.chunk - 1) / p.chunk;
+  const int nchunks = p.nchunk_max == 1 ? 1 : (len + p.chunk - 1) / p.chunk;
   if (chunk >= nchunks) return;  // uniform over the workgroup
   const int t_end = min(t_begin + p.chunk, len);
 
@@ -582,8 +639,8 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
       if (new_begin >= t_begin && new_begin < t_end && wave == kWaves - 1) {
         const bool ok[1] = {g == 0};
         softmax_step<DT, LPT, EPL, 1>(qv, &nk, &nv, ok, p.scale_log2, m, l, acc);
-        if (g == 0 && h % p.group == 0) {
-          const int bi = new_begin / p.bs;
+        if (g == 0 && (p.group == 1 || h % p.group == 0)) {
+          const int bi = FAST ? new_begin >> p.bs_shift : new_begin / p.bs;
           const int blk = s_blk[bi - first_blk];
           if (blk >= 0) {
             const int64_t dst = ((int64_t)blk * p.bs + (new_begin - bi * p.bs)) * p.row_vecs + base;
@@ -826,10 +883,27 @@ int32_t pick_chunk(int32_t rows, int32_t heads, int32_t d, int32_t max_len, int3
 
 bool supported_d(int32_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
 
+// Compute units of the current device (0 when the query fails), cached per device.
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kMaxDevices) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+  if (dev < kMaxDevices && n > 0) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
 template <int DT, int D, bool PAGED>
 void launch_attention(const AttnParams& p, hipStream_t stream) {
   const int64_t rh = (int64_t)p.batch * p.qlen * p.heads;
-  const dim3 grid((uint32_t)rh, (uint32_t)p.nchunk_max);
+  const dim3 grid = p.grid3d ? dim3((uint32_t)p.heads, (uint32_t)(p.batch * p.qlen), (uint32_t)p.nchunk_max)
+                             : dim3((uint32_t)rh, (uint32_t)p.nchunk_max);
   const bool fast = p.kv_bytes <= kBufLimit && (!PAGED || p.bs_shift >= 0);
   if (fast) {
     hipLaunchKernelGGL((attention_kernel<DT, D, PAGED, true>), grid, dim3(64 * kWaves), 0, stream, p);
@@ -904,6 +978,16 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
   p.causal = causal ? 1 : 0;
   p.chunk = chunk;
   p.nchunk_max = nchunk_max;
+  p.grid3d = (int64_t)batch * q_len <= 65535;
+  const int64_t items = (int64_t)batch * q_len * heads;
+  const int cus = device_cu_count();
+  p.snake = p.grid3d && nchunk_max == 1 && heads >= 2 && items * heads < ((int64_t)1 << 32) && cus > 0 &&
+            (cus & (cus - 1)) == 0;
+  if (p.snake) {
+    p.cu_shift = __builtin_ctz((unsigned)cus);
+    p.items = (uint32_t)items;
+    p.heads_magic = (uint32_t)((((uint64_t)1 << 32) + (uint64_t)heads - 1) / (uint64_t)heads);
+  }
   p.scale_log2 = scale * kLog2e;
   p.part = need > 0 ? (float*)ws : nullptr;
   return SKV_OK;

@@ -168,6 +168,23 @@ def test_paged_attention_config2_full_size(cuda):
     print(f"config2 paged attention max abs err {err:.3e}")
 
 
+@pytest.mark.parametrize("bsz,h", [(20, 20), (13, 31), (64, 20), (3, 2), (100, 3)])
+def test_paged_attention_every_row_head_once(cuda, bsz, h):
+    """Grids of rows x heads workgroups that end in a full, a partial even and a partial odd round of
+    workgroups per compute unit (the launch maps workgroups to (row, head) items in rounds, the odd ones
+    reversed): every (row, head) output matches the oracle, rows sorted longest-first as the engine sends them."""
+    gen = torch.Generator().manual_seed(1000 + bsz * h)
+    d, bs, nb = 64, 16, bsz * 13
+    ctx = torch.randint(1, 200, (bsz,), generator=gen).sort(descending=True).values.to(torch.int32)
+    tables = make_tables(gen, bsz, nb, 13)
+    kp, vp = make_pool(gen, nb, bs, h, d, torch.float16, cuda)
+    q = torch.randn(bsz, h, d, generator=gen).to(cuda, torch.float16)
+    out = native.paged_attention(q, kp, vp, tables.to(cuda), ctx.to(cuda), 200, 0.125)
+    torch.cuda.synchronize()
+    want = O.paged_attention(f64(q)[:, None], f64(kp), f64(vp), tables.numpy(), ctx.tolist(), 0.125)[:, 0]
+    assert_close(out, want, torch.float16, f"{bsz}x{h}")
+
+
 @pytest.mark.parametrize("chunk", [64, 128, 256, 512])
 def test_paged_attention_split_sizes_agree_and_repeat(cuda, chunk):
     gen = torch.Generator().manual_seed(5)
