@@ -29,6 +29,11 @@
  *                         (eager) and :468-479 (graph), with the masks of
  *                         phase_aware_scheduler.py:884-887,964-970 and
  *                         graph_decode_buffers.py:529,537 expressed as lengths.
+ *   skv_copy_cross_kv     one launch that copies a request's encoder K/V for every
+ *                         decoder layer into its decode slot of the slot-major
+ *                         cross-attention buffer. Replaces the per-layer copy_ loop
+ *                         of GraphDecodeBuffers.assign_slot at
+ *                         speech_serving/graph_decode_buffers.py:317-327.
  *   skv_argmax            greedy sampling (first maximum) with optional on-device
  *                         token feedback per decode slot. Replaces argmax +
  *                         copy_ at speech_serving/models.py:486-487 and
@@ -111,6 +116,26 @@ SKV_API int skv_gather(const void* k_pool, const void* v_pool,
                int32_t batch, int32_t num_heads, int32_t head_dim,
                int32_t block_size, int32_t num_blocks, int32_t max_len,
                int32_t dtype, void* stream);
+
+/*
+ * skv_copy_cross_kv — encoder K/V of every decoder layer into one decode slot.
+ *   For l < n_layers, kv in {K, V}, h < num_heads, t < n_tokens:
+ *     dst[l*dst_stride_l + kv*dst_stride_kv + h*dst_stride_h + t*dst_stride_t + d]
+ *       = src_{l,kv}[h*src_stride_h + t*src_stride_t + d]
+ *   k_srcs, v_srcs : HOST arrays of n_layers device pointers (1 <= n_layers <= 64);
+ *                    every source is [num_heads, >= n_tokens, head_dim] with the
+ *                    same strides
+ *   dst            : the slot's [n_layers, 2, num_heads, >= n_tokens, head_dim] region
+ *                    (e.g. g_cross_kv[slot]); positions >= n_tokens are left as they are
+ *   head_dim * element bytes must be a power-of-two multiple of 16.
+ * Reference: graph_decode_buffers.py:317-327 (assign_slot's per-layer copies).
+ */
+SKV_API int skv_copy_cross_kv(const void* const* k_srcs, const void* const* v_srcs, int32_t n_layers,
+                              int64_t src_stride_h, int64_t src_stride_t,
+                              void* dst, int64_t dst_stride_l, int64_t dst_stride_kv,
+                              int64_t dst_stride_h, int64_t dst_stride_t,
+                              int32_t num_heads, int32_t n_tokens, int32_t head_dim,
+                              int32_t dtype, void* stream);
 
 /*
  * skv_argmax — greedy token per row: the first index of the maximum of

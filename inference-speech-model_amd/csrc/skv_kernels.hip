@@ -125,6 +125,52 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint4* __restrict__ k
 }
 
 // ---------------------------------------------------------------------------
+// Encoder K/V into a decode slot: for every (layer, K|V) source and head h the
+// first n positions (rows of D elements) are copied into the slot's region of
+// the slot-major cross-attention buffer. Grid: z = layer * 2 + kv, y = head, x
+// covers the head's n * vpr 16-byte vectors, kCopyVecs per thread (all loads
+// issued before the stores).
+// ---------------------------------------------------------------------------
+constexpr int kMaxCrossLayers = 64;
+constexpr int kCopyVecs = 4;
+
+struct CrossCopyParams {
+  const uint4* src[2 * kMaxCrossLayers];  // layer l: K at 2l, V at 2l + 1
+  int64_t ssh, sst;                       // source head / position strides, 16-byte vectors
+  uint4* dst;
+  int64_t dsl, dskv, dsh, dst_t;          // destination layer / kv / head / position strides
+  int32_t n, vpr, vpr_shift;              // positions, vectors per row, log2(vpr) (vpr is 2^k)
+};
+
+__global__ __launch_bounds__(256) void cross_copy_kernel(CrossCopyParams p) {
+  const int pair = blockIdx.z;
+  const int h = blockIdx.y;
+  const uint4* src = p.src[pair] + (int64_t)h * p.ssh;
+  uint4* dst = p.dst + (int64_t)(pair >> 1) * p.dsl + (int64_t)(pair & 1) * p.dskv + (int64_t)h * p.dsh;
+  const int64_t total = (int64_t)p.n * p.vpr;
+  const int64_t step = (int64_t)gridDim.x * 256;
+  for (int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x; i0 < total; i0 += step * kCopyVecs) {
+    uint4 v[kCopyVecs];
+#pragma unroll
+    for (int u = 0; u < kCopyVecs; ++u) {
+      const int64_t i = i0 + u * step;
+      if (i < total) {
+        const int64_t t = i >> p.vpr_shift;
+        v[u] = src[t * p.sst + (i & (p.vpr - 1))];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyVecs; ++u) {
+      const int64_t i = i0 + u * step;
+      if (i < total) {
+        const int64_t t = i >> p.vpr_shift;
+        dst[t * p.dst_t + (i & (p.vpr - 1))] = v[u];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
 // (NaN counts as the maximum, as in torch.argmax). Optionally also writes the
 // token to slot_tokens[row_slots[r]] (skipped when the slot is negative).
@@ -1056,6 +1102,52 @@ int skv_gather(const void* k_pool, const void* v_pool, const int32_t* block_tabl
                      (uint4*)k_out, (uint4*)(v_out ? v_out : k_out), batch, num_heads, vpr, block_size, num_blocks,
                      max_len);
   return check_launch("skv_gather");
+}
+
+int skv_copy_cross_kv(const void* const* k_srcs, const void* const* v_srcs, int32_t n_layers, int64_t src_stride_h,
+                      int64_t src_stride_t, void* dst, int64_t dst_stride_l, int64_t dst_stride_kv,
+                      int64_t dst_stride_h, int64_t dst_stride_t, int32_t num_heads, int32_t n_tokens,
+                      int32_t head_dim, int32_t dtype, void* stream) {
+  const int eb = elt_bytes(dtype);
+  if (eb == 0) return fail(SKV_EDTYPE, "skv_copy_cross_kv: unknown dtype %d", dtype);
+  if (n_layers <= 0 || n_layers > kMaxCrossLayers || num_heads <= 0 || num_heads > 65535 || head_dim <= 0 ||
+      n_tokens < 0)
+    return fail(SKV_EINVAL, "skv_copy_cross_kv: bad sizes layers=%d (1..%d) heads=%d head_dim=%d n=%d", n_layers,
+                kMaxCrossLayers, num_heads, head_dim, n_tokens);
+  if (n_tokens == 0) return SKV_OK;
+  if (!k_srcs || !v_srcs || !dst) return fail(SKV_EINVAL, "skv_copy_cross_kv: null pointer argument");
+  const int epl = 16 / eb;
+  const int vpr = head_dim / epl;
+  if (head_dim % epl || (vpr & (vpr - 1)))
+    return fail(SKV_EALIGN, "skv_copy_cross_kv: head_dim*%d bytes must be a power-of-two multiple of 16", eb);
+  if (src_stride_h % epl || src_stride_t % epl || dst_stride_l % epl || dst_stride_kv % epl || dst_stride_h % epl ||
+      dst_stride_t % epl)
+    return fail(SKV_EALIGN, "skv_copy_cross_kv: strides must be multiples of %d elements", epl);
+  CrossCopyParams p{};
+  for (int l = 0; l < n_layers; ++l) {
+    if (!k_srcs[l] || !v_srcs[l]) return fail(SKV_EINVAL, "skv_copy_cross_kv: null source for layer %d", l);
+    if (!aligned16(k_srcs[l]) || !aligned16(v_srcs[l]))
+      return fail(SKV_EALIGN, "skv_copy_cross_kv: sources must be 16-byte aligned");
+    p.src[2 * l] = (const uint4*)k_srcs[l];
+    p.src[2 * l + 1] = (const uint4*)v_srcs[l];
+  }
+  if (!aligned16(dst)) return fail(SKV_EALIGN, "skv_copy_cross_kv: destination must be 16-byte aligned");
+  p.ssh = src_stride_h / epl;
+  p.sst = src_stride_t / epl;
+  p.dst = (uint4*)dst;
+  p.dsl = dst_stride_l / epl;
+  p.dskv = dst_stride_kv / epl;
+  p.dsh = dst_stride_h / epl;
+  p.dst_t = dst_stride_t / epl;
+  p.n = n_tokens;
+  p.vpr = vpr;
+  p.vpr_shift = __builtin_ctz((unsigned)vpr);
+  const int64_t per_head = (int64_t)n_tokens * vpr;
+  int64_t bx = cdiv(per_head, 256 * kCopyVecs);
+  if (bx > 65535) bx = 65535;
+  hipLaunchKernelGGL(cross_copy_kernel, dim3((uint32_t)bx, (uint32_t)num_heads, (uint32_t)(2 * n_layers)), dim3(256),
+                     0, (hipStream_t)stream, p);
+  return check_launch("skv_copy_cross_kv");
 }
 
 int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab, int32_t dtype,

@@ -195,10 +195,10 @@ class GraphDecodeBuffers:
         s.last_readback_trace = []
         s.block_table = table
 
-        for l, (ck, cv) in enumerate(enc_kv_layers[: self.num_decoder_layers]):
-            n = min(ck.shape[2], self.max_enc_len)
-            self.g_cross_kv[slot_idx, l, 0, :, :n].copy_(ck[0, :, :n])
-            self.g_cross_kv[slot_idx, l, 1, :, :n].copy_(cv[0, :, :n])
+        layers = enc_kv_layers[: self.num_decoder_layers]
+        if layers:  # every layer's encoder K/V into the slot in one launch
+            native.copy_cross_kv([ck[0] for ck, _ in layers], [cv[0] for _, cv in layers], self.g_cross_kv[slot_idx],
+                                 min(layers[0][0].shape[2], self.max_enc_len))
         row = torch.full((self.max_blocks,), -1, dtype=torch.int32)
         row[: len(table)] = torch.tensor(table, dtype=torch.int32)
         self.g_tables[slot_idx].copy_(row.to(self.device))

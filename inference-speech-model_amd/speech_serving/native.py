@@ -15,7 +15,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
-from typing import Dict, Optional, Tuple
+from typing import Dict, Optional, Sequence, Tuple
 
 import torch
 
@@ -35,6 +35,8 @@ SIGNATURES = {
     "skv_gather": (_c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                             _c_i32, _c_i32, _c_p]),
     "skv_argmax": (_c_int, [_c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p]),
+    "skv_copy_cross_kv": (_c_int, [_c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32,
+                                   _c_i32, _c_i32, _c_i32, _c_p]),
     "skv_attention_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "skv_default_chunk_tokens": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "skv_paged_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p,
@@ -206,6 +208,57 @@ def append(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_pool: torch.Ten
                           _ptr(v_pool), slot_mapping.data_ptr(), n, h, d, num_slots, _code(k_pool.dtype),
                           _stream(k_pool.device))
     _check(rc, "skv_append")
+
+
+MAX_CROSS_LAYERS = 64  # layers per skv_copy_cross_kv launch
+
+
+def copy_cross_kv(k_srcs: Sequence[torch.Tensor], v_srcs: Sequence[torch.Tensor], dst: torch.Tensor,
+                  n_tokens: int) -> None:
+    """dst[l, 0, :, :n] = k_srcs[l][:, :n] and dst[l, 1, :, :n] = v_srcs[l][:, :n] for every layer l, in one
+    launch per 64 layers.
+
+    k_srcs, v_srcs: per-layer [H, T, D] tensors (D contiguous; cast to dst's dtype when they differ).
+    dst: the slot's [L, 2, H, T_max, D] region of the slot-major cross-attention buffer (D contiguous).
+    Same bytes as GraphDecodeBuffers.assign_slot's per-layer copy_ loop in the reference
+    (speech_serving/graph_decode_buffers.py:317-327).
+    """
+    if len(k_srcs) != len(v_srcs) or not k_srcs:
+        raise RuntimeError("copy_cross_kv: k_srcs and v_srcs must be non-empty lists of equal length")
+    _gpu(dst, "dst")
+    if dst.dim() != 5 or dst.shape[1] != 2 or dst.stride(4) != 1 or dst.shape[0] < len(k_srcs):
+        raise RuntimeError(f"copy_cross_kv: dst must be [L>={len(k_srcs)}, 2, H, T, D] with D contiguous, "
+                           f"got {tuple(dst.shape)}")
+    _, _, h, t_max, d = dst.shape
+    if not 0 <= n_tokens <= t_max:
+        raise RuntimeError(f"copy_cross_kv: n_tokens {n_tokens} outside [0, {t_max}]")
+    srcs = []
+    for k, v in zip(k_srcs, v_srcs):
+        pair = []
+        for x, name in ((k, "k_srcs"), (v, "v_srcs")):
+            _gpu(x, name)
+            if x.dim() != 3 or x.shape[0] != h or x.shape[2] != d or x.shape[1] < n_tokens:
+                raise RuntimeError(f"copy_cross_kv: {name} entries must be [{h}, >={n_tokens}, {d}], "
+                                   f"got {tuple(x.shape)}")
+            if x.dtype != dst.dtype or x.stride(2) != 1:
+                x = x[:, :n_tokens].to(dst.dtype).contiguous()
+            pair.append(x)
+        srcs.append(tuple(pair))
+    if n_tokens == 0:
+        return
+    if len({(x.stride(0), x.stride(1)) for pr in srcs for x in pr}) != 1:  # one stride pair per launch
+        srcs = [tuple(x[:, :n_tokens].contiguous() for x in pr) for pr in srcs]
+    sh, st = srcs[0][0].stride(0), srcs[0][0].stride(1)
+    for l0 in range(0, len(srcs), MAX_CROSS_LAYERS):
+        part = srcs[l0:l0 + MAX_CROSS_LAYERS]
+        kp = (ctypes.c_void_p * len(part))(*[k.data_ptr() for k, _ in part])
+        vp = (ctypes.c_void_p * len(part))(*[v.data_ptr() for _, v in part])
+        base = dst[l0]
+        rc = lib().skv_copy_cross_kv(ctypes.cast(kp, ctypes.c_void_p), ctypes.cast(vp, ctypes.c_void_p), len(part),
+                                     sh, st, base.data_ptr(), dst.stride(0), dst.stride(1),
+                                     dst.stride(2), dst.stride(3), h, n_tokens, d, _code(dst.dtype),
+                                     _stream(dst.device))
+        _check(rc, "skv_copy_cross_kv")
 
 
 def gather(k_pool: torch.Tensor, v_pool: Optional[torch.Tensor], block_tables: torch.Tensor,

@@ -127,6 +127,25 @@ def test_add_layernorm_rejects_bad_arguments():
     assert call(rows=0) == 0
 
 
+def test_copy_cross_kv_rejects_bad_arguments():
+    import ctypes as C
+    lib = native.lib()
+
+    def call(layers=2, heads=20, n=1500, d=64, dtype=native.SKV_BF16, srcs=True, stride_t=64):
+        arr = (C.c_void_p * max(layers, 1))(*([FAKE] * max(layers, 1)))
+        p = C.cast(arr, C.c_void_p) if srcs else None
+        return lib.skv_copy_cross_kv(p, p, layers, 1500 * 64, stride_t, FAKE, 2 * 20 * 1500 * 64, 20 * 1500 * 64,
+                                     1500 * 64, 64, heads, n, d, dtype, None)
+
+    assert call(dtype=9) == -2
+    assert call(layers=0) == -1 and call(layers=65) == -1
+    assert call(heads=0) == -1 and call(n=-1) == -1
+    assert call(d=48) == -3            # 96 bytes: not a power-of-two multiple of 16
+    assert call(stride_t=60) == -3     # breaks 16-byte row alignment
+    assert call(srcs=False) == -1
+    assert call(n=0) == 0              # nothing to copy, no launch
+
+
 def test_python_wrapper_refuses_cpu_tensors():
     import torch
 
