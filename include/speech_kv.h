@@ -142,15 +142,27 @@ SKV_API int skv_copy_cross_kv(const void* const* k_srcs, const void* const* v_sr
  * logits[r, 0:vocab] (a NaN counts as the maximum), as torch.argmax(dim=-1).
  *   logits     : [rows, row_stride] of dtype, row_stride >= vocab
  *   out_tokens : int64 [rows]
- *   row_slots, slot_tokens (optional, both or neither): also store the token
- *                at slot_tokens[row_slots[r]] (skipped for a negative slot) —
+ *   row_slots  : int32 [rows] (optional) — the decode slot of each row; rows
+ *                whose slot is outside [0, num_slots) get no per-slot output.
+ *                Required by, and only used with, the two options below.
+ *   slot_tokens: int64 [num_slots] (optional) — slot_tokens[row_slots[r]] = token,
  *                the on-device token feedback of a graph decode step.
+ *   slot_eos, slot_finished, finished_count (optional, all or none):
+ *                int64 [num_slots] EOS id per slot (< 0: none), int32 [num_slots]
+ *                finished flags, int64 [1] counter. When a row's token is its
+ *                slot's EOS id and the slot's flag is 0, the flag becomes 1 and
+ *                the counter grows by 1. A host that copies the counter back
+ *                with the step's tokens learns of a finished request without
+ *                reading every token. Rows of one launch must name distinct
+ *                slots, except slots whose EOS id is negative.
  * Reference: speech_serving/models.py:486-487; phase_aware_scheduler.py:693,
- * 997, 1026.
+ * 997, 1026 (greedy); the EOS stop at :739-766 and the unused g_finished /
+ * g_lengths state at graph_decode_buffers.py:209-211, 556-558.
  */
 SKV_API int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab,
                        int32_t dtype, int64_t* out_tokens, const int32_t* row_slots,
-                       int64_t* slot_tokens, void* stream);
+                       int32_t num_slots, int64_t* slot_tokens, const int64_t* slot_eos,
+                       int32_t* slot_finished, int64_t* finished_count, void* stream);
 
 /*
  * Workspace bytes needed by skv_paged_attention / skv_dense_attention for a

@@ -172,8 +172,10 @@ __global__ __launch_bounds__(256) void cross_copy_kernel(CrossCopyParams p) {
 
 // ---------------------------------------------------------------------------
 // Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
-// (NaN counts as the maximum, as in torch.argmax). Optionally also writes the
-// token to slot_tokens[row_slots[r]] (skipped when the slot is negative).
+// (NaN counts as the maximum, as in torch.argmax). Optionally, for a row whose
+// slot s = row_slots[r] is in [0, num_slots): slot_tokens[s] = token (the next
+// step's input), and when the token is the slot's EOS id (slot_eos[s] >= 0) and
+// the slot is not yet finished, slot_finished[s] = 1 and finished_count += 1.
 // One 1024-thread workgroup per row reads the row as 32-bit words through a
 // buffer descriptor (past-the-end words read as zero and are not compared),
 // kArgmaxWords words per thread in flight; a 16-bit row that starts in the
@@ -196,11 +198,19 @@ template <> __device__ __forceinline__ float half_word<SKV_BF16>(uint32_t w, int
   return __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
 }
 
+struct SlotFeedback {
+  const int32_t* row_slots;  // NULL: no per-slot output
+  int32_t num_slots;
+  int64_t* slot_tokens;      // optional
+  const int64_t* slot_eos;   // optional, with slot_finished and finished_count
+  int32_t* slot_finished;
+  unsigned long long* finished_count;
+};
+
 template <int DT>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __restrict__ logits, int64_t row_bytes,
                                                                 int32_t vocab, int64_t* __restrict__ out,
-                                                                const int32_t* __restrict__ row_slots,
-                                                                int64_t* __restrict__ slot_tokens) {
+                                                                SlotFeedback f) {
   __shared__ float s_v[kArgmaxThreads / 64];
   __shared__ int s_i[kArgmaxThreads / 64];
   const int r = blockIdx.x;
@@ -261,9 +271,17 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
     for (int w = 1; w < kArgmaxThreads / 64; ++w) consider(s_v[w], s_i[w]);
     const int64_t tok = bi == 0x7fffffff ? 0 : bi;
     out[r] = tok;
-    if (row_slots) {
-      const int slot = row_slots[r];
-      if (slot >= 0) slot_tokens[slot] = tok;
+    if (f.row_slots) {
+      const int slot = f.row_slots[r];
+      if (slot >= 0 && slot < f.num_slots) {
+        if (f.slot_tokens) f.slot_tokens[slot] = tok;
+        // Rows name distinct slots within one launch (idle rows name a slot with no EOS), so the
+        // finished flag has one writer; the count is shared.
+        if (f.slot_eos && f.slot_eos[slot] >= 0 && tok == f.slot_eos[slot] && f.slot_finished[slot] == 0) {
+          f.slot_finished[slot] = 1;
+          atomicAdd(f.finished_count, 1ull);
+        }
+      }
     }
   }
 }
@@ -1151,29 +1169,33 @@ int skv_copy_cross_kv(const void* const* k_srcs, const void* const* v_srcs, int3
 }
 
 int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t vocab, int32_t dtype,
-               int64_t* out_tokens, const int32_t* row_slots, int64_t* slot_tokens, void* stream) {
+               int64_t* out_tokens, const int32_t* row_slots, int32_t num_slots, int64_t* slot_tokens,
+               const int64_t* slot_eos, int32_t* slot_finished, int64_t* finished_count, void* stream) {
   const int eb = elt_bytes(dtype);
   if (eb == 0) return fail(SKV_EDTYPE, "skv_argmax: unknown dtype %d", dtype);
-  if (rows < 0 || vocab <= 0 || vocab >= (1 << 29) || row_stride < vocab)
-    return fail(SKV_EINVAL, "skv_argmax: bad sizes rows=%d vocab=%d row_stride=%lld", rows, vocab,
-                (long long)row_stride);
+  if (rows < 0 || vocab <= 0 || vocab >= (1 << 29) || row_stride < vocab || num_slots < 0)
+    return fail(SKV_EINVAL, "skv_argmax: bad sizes rows=%d vocab=%d row_stride=%lld num_slots=%d", rows, vocab,
+                (long long)row_stride, num_slots);
   if (rows == 0) return SKV_OK;
-  if (!logits || !out_tokens || ((row_slots == nullptr) != (slot_tokens == nullptr)))
+  const bool eos = slot_eos || slot_finished || finished_count;
+  if (!logits || !out_tokens || (eos && !(slot_eos && slot_finished && finished_count)) ||
+      ((slot_tokens || eos) && !row_slots) || (row_slots && !slot_tokens && !eos))
     return fail(SKV_EINVAL, "skv_argmax: null pointer argument");
+  SlotFeedback f{row_slots, num_slots, slot_tokens, slot_eos, slot_finished, (unsigned long long*)finished_count};
   const int64_t rb = row_stride * eb;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case SKV_F32:
       hipLaunchKernelGGL(argmax_kernel<SKV_F32>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
-                         out_tokens, row_slots, slot_tokens);
+                         out_tokens, f);
       break;
     case SKV_F16:
       hipLaunchKernelGGL(argmax_kernel<SKV_F16>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
-                         out_tokens, row_slots, slot_tokens);
+                         out_tokens, f);
       break;
     default:
       hipLaunchKernelGGL(argmax_kernel<SKV_BF16>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
-                         out_tokens, row_slots, slot_tokens);
+                         out_tokens, f);
       break;
   }
   return check_launch("skv_argmax");

@@ -132,15 +132,25 @@ class GraphDecodeBuffers:
         # Row S of the tables / tokens is the spare slot idle rows point at.
         self.g_tables = torch.full((S + 1, self.max_blocks), -1, dtype=torch.int32, device=dev)
         self.g_slot_tokens = torch.zeros(S + 1, dtype=torch.int64, device=dev)
+        # On-device EOS (the reference's g_finished state): per-slot EOS id (-1 = none) and finished flag. The
+        # argmax of every step sets a slot's flag when it emits the slot's EOS id and counts it in
+        # g_output_tokens[bmax], which travels to the host with the step's tokens.
+        self.g_slot_eos = torch.full((S + 1,), -1, dtype=torch.int64, device=dev)
+        self.g_slot_finished = torch.zeros(S + 1, dtype=torch.int32, device=dev)
         bmax = self.buckets[-1]
         self.g_rows = torch.zeros((4, bmax), dtype=torch.int32, device=dev)  # slot, ctx, enc_len, cross slot
-        self.g_output_tokens = torch.zeros(bmax, dtype=torch.int64, device=dev)
+        self.g_output_tokens = torch.zeros(bmax + 1, dtype=torch.int64, device=dev)  # tokens, then finished count
 
-        self._n_banks = max(self.readback_k, 2)
+        # Two row banks: the host runs at most two steps ahead of the GPU, so a finished count that reaches
+        # the host ring (see should_readback) is seen within about two steps whatever readback_k is.
+        self._n_banks = 2
         self._banks = [torch.zeros((4, bmax), dtype=torch.int32).pin_memory() for _ in range(self._n_banks)]
         self._bank_events = [torch.cuda.Event() for _ in range(self._n_banks)]
         self._bank_in_flight = [False] * self._n_banks
-        self.h_token_ring = torch.zeros((self.readback_k, bmax), dtype=torch.int64).pin_memory()
+        self.h_token_ring = torch.zeros((self.readback_k, bmax + 1), dtype=torch.int64).pin_memory()
+        self._ring_events = [torch.cuda.Event() for _ in range(self.readback_k)]
+        self._finished_seen = 0
+        self.early_readbacks = 0
         self._readback_event = torch.cuda.Event()
         self._step_in_k = 0
         self._step_counter = 0
@@ -209,6 +219,9 @@ class GraphDecodeBuffers:
                 native.append(sk[0, :, :p].transpose(0, 1), sv[0, :, :p].transpose(0, 1), self.bm.key_pool[l],
                               self.bm.value_pool[l], slots)
         self.g_slot_tokens[slot_idx].fill_(int(initial_tok))
+        eos = getattr(req, "eos_token_id", None)
+        self.g_slot_eos[slot_idx].fill_(int(eos) if eos is not None and eos >= 0 else -1)
+        self.g_slot_finished[slot_idx].zero_()
         return slot_idx
 
     def release_slot(self, slot_idx: int) -> None:
@@ -235,7 +248,10 @@ class GraphDecodeBuffers:
                         [self.g_cross_kv[:, l, 1] for l in range(self.num_decoder_layers)],
                         enc, self.max_enc_len, slot_ids=cslot)
         logits = self.model.decode_step_paged(ids, kv, cross)
-        native.argmax(logits, out=self.g_output_tokens[:bucket], row_slots=row_slot, slot_tokens=self.g_slot_tokens)
+        bmax = self.buckets[-1]
+        native.argmax(logits, out=self.g_output_tokens[:bucket], row_slots=row_slot, slot_tokens=self.g_slot_tokens,
+                      slot_eos=self.g_slot_eos, slot_finished=self.g_slot_finished,
+                      finished_count=self.g_output_tokens[bmax:])
 
     def _idle_rows(self) -> None:
         idle = torch.zeros((4, self.g_rows.shape[1]), dtype=torch.int32)
@@ -313,8 +329,9 @@ class GraphDecodeBuffers:
             self.capture_all_buckets()
         self.graphs[bucket].replay()
         if self._step_in_k < self.h_token_ring.shape[0]:
-            self.h_token_ring[self._step_in_k, :bucket].copy_(self.g_output_tokens[:bucket],
-                                                              non_blocking=self.non_blocking_copies)
+            # Every row plus the finished count: one small copy per step, as before.
+            self.h_token_ring[self._step_in_k].copy_(self.g_output_tokens, non_blocking=self.non_blocking_copies)
+            self._ring_events[self._step_in_k].record()
             self._window_buckets.append(bucket)
             self._window_rows.append(getattr(self, "_window_rows_pending", {}))
             self._step_in_k += 1
@@ -327,7 +344,21 @@ class GraphDecodeBuffers:
     def should_readback(self) -> bool:
         if self._step_counter % self.readback_k == 0 or self._step_in_k >= self.h_token_ring.shape[0]:
             return True
-        return any(s.active and s.generated_count >= s.max_new_tokens for s in self.slots)
+        if any(s.active and s.generated_count >= s.max_new_tokens for s in self.slots):
+            return True
+        return self._eos_seen_on_device()
+
+    def _eos_seen_on_device(self) -> bool:
+        """True when the newest ring entry that has already landed (checked without waiting) counts more
+        finished slots than the last readback saw: a request emitted EOS inside the window."""
+        bmax = self.buckets[-1]
+        for k in range(self._step_in_k - 1, -1, -1):
+            if self._ring_events[k].query():
+                if int(self.h_token_ring[k, bmax]) > self._finished_seen:
+                    self.early_readbacks += 1
+                    return True
+                return False
+        return False
 
     def sync_tokens(self) -> List[Tuple[SlotInfo, List[int]]]:
         """Wait for the window's replays and return each active slot's new tokens."""
@@ -335,6 +366,8 @@ class GraphDecodeBuffers:
         self._readback_event.synchronize()
         self._bank_in_flight = [False] * self._n_banks
         ring = self.h_token_ring.tolist()
+        if self._step_in_k:
+            self._finished_seen = ring[self._step_in_k - 1][self.buckets[-1]]
         results = []
         for s in self.slots:
             if not s.active:
@@ -360,5 +393,6 @@ class GraphDecodeBuffers:
     def vram_overhead_mb(self) -> float:
         """Device bytes held by the slot buffers (cross K/V, tables, tokens, row inputs)."""
         total = sum(t.numel() * t.element_size() for t in (self.g_cross_kv, self.g_tables, self.g_slot_tokens,
-                                                            self.g_rows, self.g_output_tokens))
+                                                            self.g_slot_eos, self.g_slot_finished, self.g_rows,
+                                                            self.g_output_tokens))
         return total / (1024 * 1024)

@@ -34,7 +34,7 @@ SIGNATURES = {
     "skv_append": (_c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_p]),
     "skv_gather": (_c_int, [_c_p, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                             _c_i32, _c_i32, _c_p]),
-    "skv_argmax": (_c_int, [_c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p]),
+    "skv_argmax": (_c_int, [_c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "skv_copy_cross_kv": (_c_int, [_c_p, _c_p, _c_i32, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32,
                                    _c_i32, _c_i32, _c_i32, _c_p]),
     "skv_attention_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
@@ -299,13 +299,17 @@ def gather(k_pool: torch.Tensor, v_pool: Optional[torch.Tensor], block_tables: t
 
 
 def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, row_slots: Optional[torch.Tensor] = None,
-           slot_tokens: Optional[torch.Tensor] = None) -> torch.Tensor:
+           slot_tokens: Optional[torch.Tensor] = None, slot_eos: Optional[torch.Tensor] = None,
+           slot_finished: Optional[torch.Tensor] = None, finished_count: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Greedy tokens: first index of each row's maximum, int64 [rows].
 
-    logits: [rows, vocab] (row stride may exceed vocab). With row_slots
-    (int32 [rows]) and slot_tokens (int64), also slot_tokens[row_slots[r]] =
-    token for rows whose slot is >= 0. torch.argmax(dim=-1) semantics
-    (speech_serving/models.py:486-487).
+    logits: [rows, vocab] (row stride may exceed vocab). torch.argmax(dim=-1)
+    semantics (speech_serving/models.py:486-487). Per-slot outputs for rows whose
+    slot row_slots[r] (int32 [rows]) is in [0, num_slots):
+      slot_tokens (int64 [num_slots]): slot_tokens[slot] = token;
+      slot_eos (int64 [num_slots], < 0 = none), slot_finished (int32 [num_slots]),
+      finished_count (int64 [>= 1]): a token equal to its slot's EOS id sets the
+      slot's finished flag once and adds 1 to finished_count[0].
     """
     _gpu(logits, "logits")
     if logits.dim() != 2 or logits.stride(1) != 1:
@@ -315,15 +319,38 @@ def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, row_slots: 
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)
     if out.dtype != torch.int64 or out.numel() < rows or not out.is_contiguous():
         raise RuntimeError("argmax: out must be contiguous int64 covering the rows")
-    if (row_slots is None) != (slot_tokens is None):
-        raise RuntimeError("argmax: row_slots and slot_tokens must both be given or both be None")
+    eos_args = (slot_eos, slot_finished, finished_count)
+    if any(a is not None for a in eos_args) and not all(a is not None for a in eos_args):
+        raise RuntimeError("argmax: slot_eos, slot_finished and finished_count go together")
+    want_slots = slot_tokens is not None or slot_eos is not None
+    if want_slots != (row_slots is not None):
+        raise RuntimeError("argmax: row_slots is required by, and only used with, slot_tokens / slot_eos")
+    num_slots = 0
     if row_slots is not None:
         row_slots = _i32(row_slots, "row_slots")
-        _gpu(slot_tokens, "slot_tokens")
-        if slot_tokens.dtype != torch.int64 or not slot_tokens.is_contiguous() or row_slots.numel() < rows:
-            raise RuntimeError("argmax: slot_tokens must be contiguous int64 and row_slots must cover the rows")
+        if row_slots.numel() < rows:
+            raise RuntimeError("argmax: row_slots must cover the rows")
+        sizes = []
+        if slot_tokens is not None:
+            _gpu(slot_tokens, "slot_tokens")
+            if slot_tokens.dtype != torch.int64 or not slot_tokens.is_contiguous():
+                raise RuntimeError("argmax: slot_tokens must be contiguous int64")
+            sizes.append(slot_tokens.numel())
+        if slot_eos is not None:
+            for t, n, dt in ((slot_eos, "slot_eos", torch.int64), (slot_finished, "slot_finished", torch.int32),
+                             (finished_count, "finished_count", torch.int64)):
+                _gpu(t, n)
+                if t.dtype != dt or not t.is_contiguous():
+                    raise RuntimeError(f"argmax: {n} must be contiguous {dt}")
+            if slot_finished.numel() != slot_eos.numel() or finished_count.numel() < 1:
+                raise RuntimeError("argmax: slot_finished must match slot_eos; finished_count needs one element")
+            sizes.append(slot_eos.numel())
+        if len(set(sizes)) != 1:
+            raise RuntimeError("argmax: slot_tokens and slot_eos must have one entry per slot")
+        num_slots = sizes[0]
     rc = lib().skv_argmax(logits.data_ptr(), logits.stride(0), rows, vocab, _code(logits.dtype), out.data_ptr(),
-                          _ptr(row_slots), _ptr(slot_tokens), _stream(logits.device))
+                          _ptr(row_slots), num_slots, _ptr(slot_tokens), _ptr(slot_eos), _ptr(slot_finished),
+                          _ptr(finished_count), _stream(logits.device))
     _check(rc, "skv_argmax")
     return out
 

@@ -106,10 +106,19 @@ def test_attention_rejects_bad_group():
 
 def test_argmax_rejects_bad_arguments():
     lib = native.lib()
-    assert lib.skv_argmax(FAKE, 100, 4, 100, 9, FAKE, None, None, None) == -2
-    assert lib.skv_argmax(FAKE, 50, 4, 100, native.SKV_F16, FAKE, None, None, None) == -1  # stride < vocab
-    assert lib.skv_argmax(FAKE, 100, 4, 100, native.SKV_F16, FAKE, FAKE, None, None) == -1  # half the pair
-    assert lib.skv_argmax(FAKE, 100, 0, 100, native.SKV_F16, FAKE, None, None, None) == 0  # nothing to do
+
+    def call(stride=100, rows=4, dtype=native.SKV_F16, slots=None, num_slots=0, tokens=None, eos=None,
+             finished=None, count=None):
+        return lib.skv_argmax(FAKE, stride, rows, 100, dtype, FAKE, slots, num_slots, tokens, eos, finished, count,
+                              None)
+
+    assert call(dtype=9) == -2
+    assert call(stride=50) == -1                                    # stride < vocab
+    assert call(slots=FAKE) == -1                                   # row_slots with no per-slot output
+    assert call(tokens=FAKE, num_slots=8) == -1                     # slot output without row_slots
+    assert call(slots=FAKE, num_slots=8, eos=FAKE, finished=FAKE) == -1   # EOS group incomplete
+    assert call(slots=FAKE, num_slots=-1, tokens=FAKE) == -1
+    assert call(rows=0) == 0                                        # nothing to do
 
 
 def test_add_layernorm_rejects_bad_arguments():

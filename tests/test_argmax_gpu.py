@@ -48,6 +48,35 @@ def test_argmax_strided_rows_and_slot_feedback(cuda):
     assert st[1] == st[4] == st[5] == st[6] == st[8] == -5
 
 
+def test_argmax_eos_flags_and_count(cuda):
+    """A token equal to its slot's EOS id sets the slot's finished flag once and counts it; rows whose slot has no
+    EOS id (< 0) or lies outside [0, num_slots) change nothing."""
+    vocab, n_slots = 64, 8
+    logits = torch.full((6, vocab), -1.0, dtype=torch.float16, device=cuda)
+    winners = [5, 9, 5, 33, 7, 12]
+    for r, w in enumerate(winners):
+        logits[r, w] = 1.0
+    slots = torch.tensor([0, 1, 2, 3, 7, 9], dtype=torch.int32, device=cuda)  # slot 9 is out of range
+    eos = torch.tensor([5, 9, -1, 4, 7, 5, 5, 7], dtype=torch.int64, device=cuda)
+    finished = torch.tensor([0, 1, 0, 0, 0, 0, 0, 0], dtype=torch.int32, device=cuda)  # slot 1 already finished
+    count = torch.tensor([10], dtype=torch.int64, device=cuda)
+    tokens = torch.zeros(n_slots, dtype=torch.int64, device=cuda)
+    out = native.argmax(logits, row_slots=slots, slot_tokens=tokens, slot_eos=eos, slot_finished=finished,
+                        finished_count=count)
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == winners
+    # (slot, token): (0, 5) finishes; (1, 9) was already finished; (2, 5) has no EOS; (3, 33) is not 4;
+    # (7, 7) finishes; (9, 12) is outside the slots.
+    assert finished.cpu().tolist() == [1, 1, 0, 0, 0, 0, 0, 1]
+    assert count.item() == 12
+    assert tokens.cpu().tolist() == [5, 9, 5, 33, 0, 0, 0, 7]
+    # Same step again: finished slots are not counted twice.
+    native.argmax(logits, row_slots=slots, slot_tokens=tokens, slot_eos=eos, slot_finished=finished,
+                  finished_count=count)
+    torch.cuda.synchronize()
+    assert count.item() == 12
+
+
 def test_argmax_in_graph_replays(cuda):
     x = torch.zeros(4, 51866, dtype=torch.float16, device=cuda)
     out = torch.zeros(4, dtype=torch.int64, device=cuda)

@@ -222,6 +222,46 @@ def test_graph_eos_is_trimmed_eager_keeps_it(cuda):
     assert e == base[:3] and e[-1] == eos
 
 
+def test_on_device_eos_retires_slots_inside_a_long_readback_window(cuda):
+    """With readback every 16 steps, a request that emits EOS is still retired within a few steps: the argmax
+    marks its slot finished on the device and the count reaching the host triggers an early readback. Tokens equal
+    the eager decode cut at EOS (graph mode drops the EOS token)."""
+    # N(0, 1) weights: greedy streams that keep finding new tokens, with top-2 logit margins >= 0.09 (checked
+    # with the oracle), so every request gets an EOS position several steps in.
+    m = random_model(cuda, 405, vocab_size=100).init_normal_(1.0, seed=405)
+    gen = torch.Generator().manual_seed(405)
+    mels = [torch.randn(80, 150 + 20 * i, generator=gen).to(cuda) for i in range(6)]
+    prompt = torch.tensor([[1, 2]])
+
+    def run(graph, eos_ids, k=16):
+        enc, dec = pools(m, cuda)
+        kw = dict(graph_decode=True, graph_readback_k=k) if graph else {}
+        s = PhaseAwareSpeechScheduler(m, DualCacheManager(enc, dec), max_batch_size=8, device=str(cuda), **kw)
+        for mel, e in zip(mels, eos_ids):
+            s.submit(mel, prompt_token_ids=prompt, max_new_tokens=40, eos_token_id=e)
+        done = sorted(s.run_until_done(), key=lambda r: r.id)
+        assert dec.allocated_block_count == 0 and enc.allocated_block_count == 0
+        return done, s
+
+    base, _ = run(False, [-1] * 6)
+    # Per request, the EOS id is the token at the last position >= 2 where a token first appears, so the
+    # request stops there (graph mode keeps the tokens before it).
+    eos_ids, cut = [], []
+    for r in base:
+        toks = r.generated_tokens
+        firsts = [p for p in range(2, len(toks)) if toks[p] not in toks[:p]]
+        pos = firsts[-1] if firsts else None
+        eos_ids.append(toks[pos] if pos is not None else -1)
+        cut.append(toks[:pos] if pos is not None else toks)
+    assert sum(e >= 0 for e in eos_ids) >= 5, ("seeded model gives too few usable EOS positions",
+                                               [r.generated_tokens for r in base])
+    done, s = run(True, eos_ids)
+    assert [r.generated_tokens for r in done] == cut
+    extra = [r.graph_extra_slot_steps for r, e in zip(done, eos_ids) if e >= 0]
+    assert max(extra) <= 5, extra          # the 16-step window alone would allow up to 15
+    assert s.graph_buffers.early_readbacks > 0
+
+
 def test_graph_slots_reused_across_lengths(cuda):
     m = random_model(cuda, 202, vocab_size=100)
     enc, dec = pools(m, cuda)
