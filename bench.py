@@ -58,8 +58,9 @@ def parse():
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--decode-tokens", type=int, default=448)
     ap.add_argument("--decode-layers", type=int, default=32)
-    ap.add_argument("--mode", choices=["attention", "copy"], default="attention",
-                    help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling")
+    ap.add_argument("--mode", choices=["attention", "copy", "decode"], default="attention",
+                    help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling; "
+                         "decode: only the large-v3-shaped greedy decode")
     ap.add_argument("--copy-mib", type=int, default=512)
     return ap.parse_args()
 
@@ -326,6 +327,10 @@ def main():
         copy_calibration(a)
         return
     dev = torch.device("cuda", 0)
+    if a.mode == "decode":  # the large-v3-shaped greedy decode alone (for kernel traces of the decode step)
+        native.lib()
+        print(json.dumps({"large_v3_decode": large_v3_decode(torch, dev, a)}))
+        return
     dtype = torch.float16
     scale = 1.0 / math.sqrt(a.head_dim)
     native.lib()

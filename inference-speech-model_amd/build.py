@@ -41,6 +41,9 @@ def build(debug: bool = False, verbose: bool = False) -> str:
         "-shared",
         # Packed fp32 VALU ops are kept out of every kernel on purpose.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # The first 16 kernel-argument dwords arrive in scalar registers when a
+        # wave starts (the attention kernel puts its address-chain parameters there).
+        "-mllvm", "-amdgpu-kernarg-preload-count=16",
         "-fvisibility=hidden",
         "-I", INCLUDE,
         "-I", CSRC,

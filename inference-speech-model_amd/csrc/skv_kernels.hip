@@ -568,8 +568,20 @@ __device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off
 // Grid: x = query row * heads + head, y = key chunk. FAST: the buffer path;
 // for paged K/V it also needs a power-of-two block size (p.bs_shift), so
 // key -> (block, offset) is a shift and a mask.
+// The parameters of the prologue's address chain come first, as separate
+// scalar arguments: the build preloads the first 14 argument dwords into
+// scalar registers when the wave starts, so the chain's first memory access
+// (block table, row length) does not wait for a kernel-argument load.
+// qlen_group: q_len in bits 0-15, query heads per KV head in bits 16-31.
+// flags: bit 0 grid3d, bit 1 snake order, bit 2 causal, bits 8-15 cu_shift,
+// bits 16-23 log2(block size) (the fast path's power-of-two block size).
 template <int DT, int D, bool PAGED, bool FAST>
-__global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * kWaves) void attention_kernel(const int32_t* __restrict__ a_tables,
+                                                               const int32_t* __restrict__ a_lens,
+                                                               const int32_t* __restrict__ a_trows, int32_t heads,
+                                                               int32_t tstride, int32_t max_len, int32_t chunk_len,
+                                                               uint32_t qlen_group, uint32_t flags, uint32_t items,
+                                                               uint32_t heads_magic, AttnParams p) {
   constexpr int EPL = Elt<DT>::EPL;
   constexpr int LPT = D / EPL;
   constexpr int TPI = 64 / LPT;
@@ -583,61 +595,55 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  // Every parameter on the prologue's address chain, read in one scalar batch:
-  // left alone, the compiler spreads these reads over several waits, each a
-  // scalar memory round trip before the first K/V load can issue.
-  // The asm has no memory effects (so the loads behind it keep their scalar
-  // form) and its zero output feeds the workgroup index, which places it first.
-  uint32_t batch0;
-  asm("s_mov_b32 %0, 0"
-      : "=s"(batch0)
-      : "s"(p.lens), "s"(p.trows), "s"(p.tables), "s"(p.q), "s"(p.qsb), "s"(p.qsh), "s"(p.heads), "s"(p.qlen),
-        "s"(p.group), "s"(p.snake), "s"(p.cu_shift), "s"(p.items), "s"(p.heads_magic), "s"(p.grid3d),
-        "s"(p.tstride), "s"(p.chunk), "s"(p.max_len), "s"(p.causal), "s"(p.bs), "s"(p.nb));
-  uint32_t batch1;
-  asm("s_mov_b32 %0, 0"
-      : "=s"(batch1)
-      : "s"(p.qsq), "s"(p.o), "s"(p.osb), "s"(p.osq), "s"(p.osh), "s"(p.k), "s"(p.v), "s"(p.bs_shift),
-        "s"(p.row_vecs), "s"(p.kv_bytes), "s"(p.kn), "s"(p.vn), "s"(p.nsb), "s"(p.nsh), "s"(p.nchunk_max),
-        "s"(p.scale_log2));
-  const uint32_t bx = blockIdx.x + batch0 + batch1;
+  const uint32_t bx = blockIdx.x;
+  const int qlen = (int)(qlen_group & 0xffffu), group = (int)(qlen_group >> 16);
+  const bool causal = (flags >> 2) & 1u;
+  const uint32_t cu_shift = (flags >> 8) & 0xffu;
+  const int bs_shift = (int)((flags >> 16) & 0xffu);
+  // Keys visible to query qi of batch row b.
+  auto visible = [&](int b, int qi) {
+    int len = a_lens[b];
+    if (causal) len -= (qlen - 1 - qi);
+    len = len < 0 ? 0 : len;
+    return len > max_len ? max_len : len;
+  };
   // Grid (heads, rows, chunks), or (rows * heads, chunks) when the rows exceed
   // the y limit. Every wave of a CU's resident workgroups runs this prologue on
   // the CU's one scalar unit before its first memory access, so the common
   // shapes (q_len 1, no KV grouping, one chunk) take no integer division.
   int h, row, chunk;
-  if (p.snake) {
-    const uint32_t w = bx + blockIdx.y * (uint32_t)p.heads;
-    const uint32_t round = (1u << p.cu_shift) - 1u;
+  if (flags & 2u) {
+    const uint32_t w = bx + blockIdx.y * (uint32_t)heads;
+    const uint32_t round = (1u << cu_shift) - 1u;
     const uint32_t base = w & ~round;
     uint32_t item = w;
-    if ((w >> p.cu_shift) & 1u) {
-      const uint32_t n = min(round + 1u, p.items - base);
+    if ((w >> cu_shift) & 1u) {
+      const uint32_t n = min(round + 1u, items - base);
       item = base + (n - 1u) - (w - base);
     }
-    row = (int)__umulhi(item, p.heads_magic);
-    h = (int)item - row * p.heads;
+    row = (int)__umulhi(item, heads_magic);
+    h = (int)item - row * heads;
     chunk = 0;
-  } else if (p.grid3d) {
+  } else if (flags & 1u) {
     h = bx;
     row = blockIdx.y;
     chunk = blockIdx.z;
   } else {
-    row = bx / p.heads;
-    h = bx - row * p.heads;
+    row = bx / heads;
+    h = bx - row * heads;
     chunk = blockIdx.y;
   }
-  const int rh = row * p.heads + h;
+  const int rh = row * heads + h;
   int b = row, qi = 0;
-  if (p.qlen != 1) {
-    b = row / p.qlen;
-    qi = row - b * p.qlen;
+  if (qlen != 1) {
+    b = row / qlen;
+    qi = row - b * qlen;
   }
   const int g = lane / LPT;
   const int j = lane - g * LPT;
   const int64_t o_off = (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh + j;
-  const int t_begin = chunk * p.chunk;
-  const int kvh = p.group == 1 ? h : h / p.group;
+  const int t_begin = chunk * chunk_len;
+  const int kvh = group == 1 ? h : h / group;
   const uint4* zero = reinterpret_cast<const uint4*>(g_zero16);
 
   // Loads in the order of the address chain: the row length and the table row
@@ -646,14 +652,14 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
   // the first K/V loads have been issued. Block ids are staged for the chunk's
   // span up to max_len (inside the table row, which covers max_len), so the
   // staging does not wait for the row length.
-  const int len = visible_len(p, b, qi);
+  const int len = visible(b, qi);
   int first_blk = 0;
   if constexpr (PAGED) {
-    const int trow = p.trows ? p.trows[b] : b;
-    const int32_t* tbl = p.tables + (int64_t)trow * p.tstride;
-    const int span_end = min(t_begin + p.chunk, p.max_len);
-    first_blk = FAST ? t_begin >> p.bs_shift : t_begin / p.bs;
-    const int last_blk = FAST ? (span_end - 1) >> p.bs_shift : (span_end - 1) / p.bs;
+    const int trow = a_trows ? a_trows[b] : b;
+    const int32_t* tbl = a_tables + (int64_t)trow * tstride;
+    const int span_end = min(t_begin + chunk_len, max_len);
+    first_blk = FAST ? t_begin >> bs_shift : t_begin / p.bs;
+    const int last_blk = FAST ? (span_end - 1) >> bs_shift : (span_end - 1) / p.bs;
     const int nblk = span_end > t_begin ? last_blk - first_blk + 1 : 0;
     for (int i = threadIdx.x; i < nblk; i += 64 * kWaves) {
       const int blk = tbl[first_blk + i];
@@ -665,7 +671,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
   // the new K/V row here, with q, scores it before the pool loop and writes it
   // to the pool from registers, so the append adds no memory round trip. Its
   // kn/vn address does not depend on the row length.
-  const bool one_new = PAGED && p.kn && p.qlen == 1;
+  const bool one_new = PAGED && p.kn && qlen == 1;
   uint4 nk = make_uint4(0u, 0u, 0u, 0u), nv = nk;
   if (one_new && wave == kWaves - 1 && g == 0) {
     const int64_t noff = (int64_t)b * p.nsb + (int64_t)kvh * p.nsh + j;
@@ -677,9 +683,9 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
     if (chunk == 0 && wave == 0 && g == 0) p.o[o_off] = make_uint4(0u, 0u, 0u, 0u);
     return;
   }
-  const int nchunks = p.nchunk_max == 1 ? 1 : (len + p.chunk - 1) / p.chunk;
+  const int nchunks = p.nchunk_max == 1 ? 1 : (len + chunk_len - 1) / chunk_len;
   if (chunk >= nchunks) return;  // uniform over the workgroup
-  const int t_end = min(t_begin + p.chunk, len);
+  const int t_end = min(t_begin + chunk_len, len);
 
   // Keys [t_begin, pool_end) are read from K/V; with a fused append the
   // newest keys [new_begin, len) come from kn/vn instead (fresh loop below).
@@ -694,7 +700,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
     __syncthreads();
     base = (int64_t)kvh * LPT + j;
     if (p.kn) {
-      new_begin = visible_len(p, b, p.qlen - 1) - p.qlen;
+      new_begin = visible(b, qlen - 1) - qlen;
       pool_end = max(t_begin, min(new_begin, t_end));
     }
     if (one_new) {
@@ -703,8 +709,8 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
       if (new_begin >= t_begin && new_begin < t_end && wave == kWaves - 1) {
         const bool ok[1] = {g == 0};
         softmax_step<DT, LPT, EPL, 1>(qv, &nk, &nv, ok, p.scale_log2, m, l, acc);
-        if (g == 0 && (p.group == 1 || h % p.group == 0)) {
-          const int bi = FAST ? new_begin >> p.bs_shift : new_begin / p.bs;
+        if (g == 0 && (group == 1 || h % group == 0)) {
+          const int bi = FAST ? new_begin >> bs_shift : new_begin / p.bs;
           const int blk = s_blk[bi - first_blk];
           if (blk >= 0) {
             const int64_t dst = ((int64_t)blk * p.bs + (new_begin - bi * p.bs)) * p.row_vecs + base;
@@ -716,7 +722,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
     } else if (p.kn) {
       // Append: the last query row's workgroups of the first head of each KV
       // group write the new keys of their chunk into the pool.
-      if (qi == p.qlen - 1 && h % p.group == 0) {
+      if (qi == qlen - 1 && h % group == 0) {
         const int w0 = max(new_begin, t_begin);
         const int nw = t_end - w0;
         for (int i = threadIdx.x; i < 2 * nw * LPT; i += 64 * kWaves) {
@@ -763,10 +769,10 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(AttnParams p) {
         bool valid = t < pool_end;
         uint32_t row = (uint32_t)t;
         if constexpr (PAGED) {
-          const int bi = t >> p.bs_shift;
+          const int bi = t >> bs_shift;
           const int blk = s_blk[min(bi - first_blk, kMaxChunkBlocks - 1)];
           valid = valid && blk >= 0;
-          row = ((uint32_t)blk << p.bs_shift) | (uint32_t)(t & (p.bs - 1));
+          row = ((uint32_t)blk << bs_shift) | (uint32_t)(t & ((1 << bs_shift) - 1));
         }
         off[u] = valid ? row * row_bytes + col_bytes : kBufOutOfRange;
         ok[u] = valid;
@@ -969,10 +975,15 @@ void launch_attention(const AttnParams& p, hipStream_t stream) {
   const dim3 grid = p.grid3d ? dim3((uint32_t)p.heads, (uint32_t)(p.batch * p.qlen), (uint32_t)p.nchunk_max)
                              : dim3((uint32_t)rh, (uint32_t)p.nchunk_max);
   const bool fast = p.kv_bytes <= kBufLimit && (!PAGED || p.bs_shift >= 0);
+  const uint32_t qlen_group = (uint32_t)p.qlen | ((uint32_t)p.group << 16);
+  const uint32_t flags = (p.grid3d ? 1u : 0u) | (p.snake ? 2u : 0u) | (p.causal ? 4u : 0u) |
+                         ((uint32_t)p.cu_shift << 8) | ((uint32_t)(p.bs_shift & 0xff) << 16);
   if (fast) {
-    hipLaunchKernelGGL((attention_kernel<DT, D, PAGED, true>), grid, dim3(64 * kWaves), 0, stream, p);
+    hipLaunchKernelGGL((attention_kernel<DT, D, PAGED, true>), grid, dim3(64 * kWaves), 0, stream, p.tables, p.lens,
+                       p.trows, p.heads, p.tstride, p.max_len, p.chunk, qlen_group, flags, p.items, p.heads_magic, p);
   } else {
-    hipLaunchKernelGGL((attention_kernel<DT, D, PAGED, false>), grid, dim3(64 * kWaves), 0, stream, p);
+    hipLaunchKernelGGL((attention_kernel<DT, D, PAGED, false>), grid, dim3(64 * kWaves), 0, stream, p.tables, p.lens,
+                       p.trows, p.heads, p.tstride, p.max_len, p.chunk, qlen_group, flags, p.items, p.heads_magic, p);
   }
   if (p.nchunk_max > 1)
     hipLaunchKernelGGL((merge_kernel<DT, D>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, stream, p);
@@ -1002,9 +1013,10 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
   const int eb = elt_bytes(dtype);
   if (eb == 0) return fail(SKV_EDTYPE, "%s: unknown dtype %d", who, dtype);
   if (!supported_d(d)) return fail(SKV_EINVAL, "%s: head_dim %d not in {16,32,64,128}", who, d);
-  if (batch < 0 || q_len <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads != 0 || max_len < 0)
-    return fail(SKV_EINVAL, "%s: bad sizes batch=%d q_len=%d heads=%d kv_heads=%d max_len=%d", who, batch, q_len,
-                heads, kv_heads, max_len);
+  if (batch < 0 || q_len <= 0 || q_len > 65535 || heads <= 0 || heads > 65535 || kv_heads <= 0 ||
+      heads % kv_heads != 0 || max_len < 0)
+    return fail(SKV_EINVAL, "%s: bad sizes batch=%d q_len=%d (1..65535) heads=%d (1..65535) kv_heads=%d max_len=%d",
+                who, batch, q_len, heads, kv_heads, max_len);
   if (!q || !k || !v || !out || !lens) return fail(SKV_EINVAL, "%s: null pointer argument", who);
   const int epl = 16 / eb;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
