@@ -55,6 +55,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-large-v3", action="store_true", help="skip the large-v3 kernel and decode measurements")
+    ap.add_argument("--no-decode", action="store_true", help="skip the large-v3 decode (keep its kernel measurements)")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--decode-tokens", type=int, default=448)
     ap.add_argument("--decode-layers", type=int, default=32)
@@ -444,7 +445,8 @@ def main():
     torch.cuda.empty_cache()
     if not a.no_large_v3:
         result.update(large_v3_kernels(torch, native, dev, a))
-        result["large_v3_decode"] = large_v3_decode(torch, dev, a)
+        if not a.no_decode:
+            result["large_v3_decode"] = large_v3_decode(torch, dev, a)
     print(json.dumps(result), flush=True)
 
 
