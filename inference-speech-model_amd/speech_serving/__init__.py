@@ -7,6 +7,7 @@ hand-written gfx950 HIP kernels (libspeechkv.so, bound in speech_serving.native)
 """
 from .block_manager import BlockManager
 from .dual_cache_manager import DualCacheManager
+from .encoder_attention import EncoderAttentionBackend
 from .encoder_block_manager import EncoderBlockManager
 from .graph_decode_buffers import GraphDecodeBuffers
 from .memory_guard import MemoryGuard
@@ -14,7 +15,7 @@ from .models import CrossKV, DecoderLayer, PagedKV, WhisperClassSpeechEncoderDec
 from .phase_aware_scheduler import DualCacheRequest, PhaseAwareSpeechScheduler, RequestPhase
 
 __all__ = [
-    "BlockManager", "DualCacheManager", "EncoderBlockManager", "GraphDecodeBuffers", "MemoryGuard",
+    "BlockManager", "DualCacheManager", "EncoderAttentionBackend", "EncoderBlockManager", "GraphDecodeBuffers", "MemoryGuard",
     "CrossKV", "DecoderLayer", "PagedKV", "WhisperClassSpeechEncoderDecoderModel", "DualCacheRequest",
     "PhaseAwareSpeechScheduler", "RequestPhase",
 ]
