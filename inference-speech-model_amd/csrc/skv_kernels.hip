@@ -4,8 +4,13 @@
 //
 // Attention design:
 //   * One workgroup of kWaves wave64s owns one (query row, head, key chunk).
-//     For paged K/V the chunk's block ids are staged once into LDS, so the
-//     K/V loads of a wave never wait on a table load.
+//     Paged fast path (power-of-two block size of at least TPI keys): each
+//     wave reads its block ids with scalar loads, one batch per trip, and no
+//     load the wave issues before its first K/V loads is waited for: a CU
+//     returns vector loads in issue order, so a vector table (or q) load of a
+//     workgroup that starts late would wait behind the K/V bytes already
+//     queued by the CU's other workgroups. General paged path: the chunk's
+//     block ids are staged once into LDS.
 //   * A 16-byte lane load carries EPL elements; LPT = D/EPL lanes cover one
 //     key row, so one wave instruction reads TPI = 64/LPT whole key rows
 //     (128 contiguous bytes each for fp16/bf16 at D=64). A wave loads K and V
@@ -418,6 +423,8 @@ void launch_add_layernorm(const AddNormParams& p, int vpl, hipStream_t s) {
 constexpr int kWaves = SKV_ATTN_WAVES;  // waves per attention workgroup
 constexpr int kMaxChunkBlocks = 256;    // LDS block-id slots per chunk
 constexpr int kPartPad = 4;             // partial record = m, l, pad, pad, acc[D]
+// s_waitcnt immediate for vmcnt(0) alone (expcnt and lgkmcnt at their maxima).
+constexpr int kWaitVmcnt0 = 0x0f70;
 
 struct AttnParams {
   const uint4* q;  // strides below are in 16-byte vector units
@@ -566,8 +573,11 @@ __device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off
 }
 
 // Grid: x = query row * heads + head, y = key chunk. FAST: the buffer path;
-// for paged K/V it also needs a power-of-two block size (p.bs_shift), so
-// key -> (block, offset) is a shift and a mask.
+// for paged K/V it also needs a power-of-two block size (p.bs_shift) of at
+// least TPI keys. Then the TPI keys one load instruction of a wave covers lie
+// in one block, so each load's block id is wave-uniform: it is read from the
+// block table with a scalar load, which travels through the scalar cache, not
+// the CU's vector memory queue.
 // The parameters of the prologue's address chain come first, as separate
 // scalar arguments: the build preloads the first 14 argument dwords into
 // scalar registers when the wave starts, so the chain's first memory access
@@ -575,13 +585,14 @@ __device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off
 // qlen_group: q_len in bits 0-15, query heads per KV head in bits 16-31.
 // flags: bit 0 grid3d, bit 1 snake order, bit 2 causal, bits 8-15 cu_shift,
 // bits 16-23 log2(block size) (the fast path's power-of-two block size).
+// Paged launches hold 5 workgroups per CU (the large decode batches fill one
+// resident generation), so the paged variants are kept within the register
+// budget of 5 waves per SIMD.
 template <int DT, int D, bool PAGED, bool FAST>
-__global__ __launch_bounds__(64 * kWaves) void attention_kernel(const int32_t* __restrict__ a_tables,
-                                                               const int32_t* __restrict__ a_lens,
-                                                               const int32_t* __restrict__ a_trows, int32_t heads,
-                                                               int32_t tstride, int32_t max_len, int32_t chunk_len,
-                                                               uint32_t qlen_group, uint32_t flags, uint32_t items,
-                                                               uint32_t heads_magic, AttnParams p) {
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAGED ? 5 : 1))) void attention_kernel(
+    const int32_t* __restrict__ a_tables, const int32_t* __restrict__ a_lens, const int32_t* __restrict__ a_trows,
+    int32_t heads, int32_t tstride, int32_t max_len, int32_t chunk_len, uint32_t qlen_group, uint32_t flags,
+    uint32_t items, uint32_t heads_magic, AttnParams p) {
   constexpr int EPL = Elt<DT>::EPL;
   constexpr int LPT = D / EPL;
   constexpr int TPI = 64 / LPT;
@@ -592,6 +603,9 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(const int32_t* _
   __shared__ int s_blk[PAGED ? kMaxChunkBlocks : 1];
   __shared__ float s_ml[kWaves][2];
   __shared__ float s_acc[kWaves][D];
+  // Fast paged path: the fused-append K/V row, copied here by the load itself
+  // (one 16-byte slot per lane of the last wave).
+  __shared__ uint4 s_new[(PAGED && FAST) ? 2 : 1][64];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -600,9 +614,9 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(const int32_t* _
   const bool causal = (flags >> 2) & 1u;
   const uint32_t cu_shift = (flags >> 8) & 0xffu;
   const int bs_shift = (int)((flags >> 16) & 0xffu);
-  // Keys visible to query qi of batch row b.
-  auto visible = [&](int b, int qi) {
-    int len = a_lens[b];
+  // Keys visible to query qi of a row whose cache holds row_len keys.
+  auto visible = [&](int row_len, int qi) {
+    int len = row_len;
     if (causal) len -= (qlen - 1 - qi);
     len = len < 0 ? 0 : len;
     return len > max_len ? max_len : len;
@@ -646,37 +660,65 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(const int32_t* _
   const int kvh = group == 1 ? h : h / group;
   const uint4* zero = reinterpret_cast<const uint4*>(g_zero16);
 
-  // Loads in the order of the address chain: the row length and the table row
-  // (scalar), then the chunk's block ids (the only load the workgroup barrier
-  // waits for), then q and the fused-append row, which are first needed after
+  // Loads in the order of the address chain. First one scalar batch: the row
+  // length, the table row and the parameter-block fields used before the
+  // first K/V load. The empty asm takes them as scalar-register operands, so
+  // every one of these loads issues before a single wait (left to itself the
+  // compiler issues each where it is first used and waits for each in turn).
+  // The asm has no memory effects, so the loads behind it keep their scalar
+  // form. Then (general path) the chunk's block ids, staged in LDS for the
+  // workgroup, then q and the fused-append row, which are first needed after
   // the first K/V loads have been issued. Block ids are staged for the chunk's
   // span up to max_len (inside the table row, which covers max_len), so the
-  // staging does not wait for the row length.
-  const int len = visible(b, qi);
+  // staging does not wait for the row length. The fast path reads block ids
+  // per wave with scalar loads in its key loop instead.
+  int row_len = a_lens[b];
+  const int trow = PAGED && a_trows ? a_trows[b] : b;
+  asm("" : "+s"(row_len)
+      : "s"(trow), "s"(p.q), "s"(p.qsb), "s"(p.qsq), "s"(p.qsh), "s"(p.osb), "s"(p.osq), "s"(p.osh),
+        "s"(p.k), "s"(p.v), "s"(p.nb), "s"(p.row_vecs), "s"(p.kv_bytes), "s"(p.kn), "s"(p.vn),
+        "s"(p.nsb), "s"(p.nsh), "s"(p.nchunk_max));
+  const int len = visible(row_len, qi);
   int first_blk = 0;
+  const int32_t* tbl = nullptr;
   if constexpr (PAGED) {
-    const int trow = a_trows ? a_trows[b] : b;
-    const int32_t* tbl = a_tables + (int64_t)trow * tstride;
-    const int span_end = min(t_begin + chunk_len, max_len);
-    first_blk = FAST ? t_begin >> bs_shift : t_begin / p.bs;
-    const int last_blk = FAST ? (span_end - 1) >> bs_shift : (span_end - 1) / p.bs;
-    const int nblk = span_end > t_begin ? last_blk - first_blk + 1 : 0;
-    for (int i = threadIdx.x; i < nblk; i += 64 * kWaves) {
-      const int blk = tbl[first_blk + i];
-      s_blk[i] = ((uint32_t)blk < (uint32_t)p.nb) ? blk : -1;
+    tbl = a_tables + (int64_t)trow * tstride;
+    if constexpr (!FAST) {
+      const int span_end = min(t_begin + chunk_len, max_len);
+      first_blk = t_begin / p.bs;
+      const int last_blk = (span_end - 1) / p.bs;
+      const int nblk = span_end > t_begin ? last_blk - first_blk + 1 : 0;
+      for (int i = threadIdx.x; i < nblk; i += 64 * kWaves) {
+        const int blk = tbl[first_blk + i];
+        s_blk[i] = ((uint32_t)blk < (uint32_t)p.nb) ? blk : -1;
+      }
     }
   }
+  // Block id of key t from the table row (fast path), -1 when invalid.
+  auto table_block = [&](int t) {
+    const int blk = tbl[t >> bs_shift];
+    return ((uint32_t)blk < (uint32_t)p.nb) ? blk : -1;
+  };
   const uint4 qv = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + j];
   // A fused append of one key (q_len 1, the decode step): the last wave loads
-  // the new K/V row here, with q, scores it before the pool loop and writes it
-  // to the pool from registers, so the append adds no memory round trip. Its
-  // kn/vn address does not depend on the row length.
+  // the new K/V row here, with q, scores it and writes it to the pool, so the
+  // append adds no memory round trip. Its kn/vn address does not depend on the
+  // row length. The fast paged path loads it straight into LDS (no registers
+  // held across the pool loop) and scores it after its pool trips; the general
+  // path loads it into registers and scores it before the pool loop.
   const bool one_new = PAGED && p.kn && qlen == 1;
   uint4 nk = make_uint4(0u, 0u, 0u, 0u), nv = nk;
   if (one_new && wave == kWaves - 1 && g == 0) {
     const int64_t noff = (int64_t)b * p.nsb + (int64_t)kvh * p.nsh + j;
-    nk = p.kn[noff];
-    nv = p.vn[noff];
+    if constexpr (PAGED && FAST) {
+      using lds_ptr = __attribute__((address_space(3))) void*;
+      using glb_ptr = __attribute__((address_space(1))) void*;
+      __builtin_amdgcn_global_load_lds((glb_ptr)(p.kn + noff), (lds_ptr)&s_new[0][0], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glb_ptr)(p.vn + noff), (lds_ptr)&s_new[1][0], 16, 0, 0);
+    } else {
+      nk = p.kn[noff];
+      nv = p.vn[noff];
+    }
   }
 
   if (len == 0) {
@@ -696,29 +738,42 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(const int32_t* _
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  // Fused append of one key: the new key is len - 1; the chunk that holds it
+  // (uniform test) scores it in the last wave, and the first head of each KV
+  // group stores it into the pool.
+  auto score_new_key = [&]() {
+    if (new_begin >= t_begin && new_begin < t_end && wave == kWaves - 1) {
+      if constexpr (PAGED && FAST) {
+        // The LDS copy has landed once this wave's loads have all completed.
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        if (g == 0) {
+          nk = s_new[0][lane];
+          nv = s_new[1][lane];
+        }
+      }
+      const bool ok[1] = {g == 0};
+      softmax_step<DT, LPT, EPL, 1>(qv, &nk, &nv, ok, p.scale_log2, m, l, acc);
+      if (g == 0 && (group == 1 || h % group == 0)) {
+        const int bi = FAST ? new_begin >> bs_shift : new_begin / p.bs;
+        const int blk = FAST ? table_block(new_begin) : s_blk[bi - first_blk];
+        if (blk >= 0) {
+          const int64_t dst = ((int64_t)blk * p.bs + (new_begin - bi * p.bs)) * p.row_vecs + base;
+          const_cast<uint4*>(p.k)[dst] = nk;
+          const_cast<uint4*>(p.v)[dst] = nv;
+        }
+      }
+    }
+  };
   if constexpr (PAGED) {
-    __syncthreads();
+    if constexpr (!FAST) __syncthreads();
     base = (int64_t)kvh * LPT + j;
     if (p.kn) {
-      new_begin = visible(b, qlen - 1) - qlen;
+      new_begin = visible(row_len, qlen - 1) - qlen;
       pool_end = max(t_begin, min(new_begin, t_end));
     }
     if (one_new) {
-      // The new key is len - 1; the chunk that holds it (uniform test) scores it
-      // in the last wave, and the first head of each KV group stores it.
-      if (new_begin >= t_begin && new_begin < t_end && wave == kWaves - 1) {
-        const bool ok[1] = {g == 0};
-        softmax_step<DT, LPT, EPL, 1>(qv, &nk, &nv, ok, p.scale_log2, m, l, acc);
-        if (g == 0 && (group == 1 || h % group == 0)) {
-          const int bi = FAST ? new_begin >> bs_shift : new_begin / p.bs;
-          const int blk = s_blk[bi - first_blk];
-          if (blk >= 0) {
-            const int64_t dst = ((int64_t)blk * p.bs + (new_begin - bi * p.bs)) * p.row_vecs + base;
-            const_cast<uint4*>(p.k)[dst] = nk;
-            const_cast<uint4*>(p.v)[dst] = nv;
-          }
-        }
-      }
+      // The fast path scores the new key after its first K/V loads are issued.
+      if constexpr (!FAST) score_new_key();
     } else if (p.kn) {
       // Append: the last query row's workgroups of the first head of each KV
       // group write the new keys of their chunk into the pool.
@@ -731,7 +786,7 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(const int32_t* _
           const int tt = w0 + r / LPT;
           const int jj = r - (r / LPT) * LPT;
           const int bi = tt / p.bs;
-          const int blk = s_blk[bi - first_blk];
+          const int blk = FAST ? table_block(tt) : s_blk[bi - first_blk];
           if (blk >= 0) {
             const int64_t dst = ((int64_t)blk * p.bs + (tt - bi * p.bs)) * p.row_vecs + (int64_t)kvh * LPT + jj;
             const int64_t src = (int64_t)b * p.nsb + (int64_t)(tt - new_begin) * p.nsq + (int64_t)kvh * p.nsh + jj;
@@ -760,33 +815,74 @@ __global__ __launch_bounds__(64 * kWaves) void attention_kernel(const int32_t* _
                                                                           (int)p.kv_bytes, kBufWord3);
     const uint32_t row_bytes = PAGED ? (uint32_t)p.row_vecs * 16u : (uint32_t)p.st * 16u;
     const uint32_t col_bytes = PAGED ? (uint32_t)base * 16u : (uint32_t)j * 16u;
-    for (int s = t_begin + wave * SUB; s < pool_end; s += kWaves * SUB) {
-      uint32_t off[U];
-      bool ok[U];
+    // Wave-uniform start, so the paged path's table reads are scalar loads.
+    const int s0 = t_begin + __builtin_amdgcn_readfirstlane(wave) * SUB;
+    if constexpr (PAGED) {
+      const uint32_t lane_off = (uint32_t)g * row_bytes + col_bytes;
+      const uint32_t bmask = (1u << bs_shift) - 1u;
+      const uint32_t blk_bytes = row_bytes << bs_shift;
+      const uint32_t last_key = (uint32_t)pool_end - 1u;
+      const uint32_t* trow = reinterpret_cast<const uint32_t*>(tbl);
+      uint32_t cu_off[U];  // ((u*TPI) & bmask) * row_bytes, wave-uniform
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int t = s + u * TPI + g;
-        bool valid = t < pool_end;
-        uint32_t row = (uint32_t)t;
-        if constexpr (PAGED) {
-          const int bi = t >> bs_shift;
-          const int blk = s_blk[min(bi - first_blk, kMaxChunkBlocks - 1)];
-          valid = valid && blk >= 0;
-          row = ((uint32_t)blk << bs_shift) | (uint32_t)(t & ((1 << bs_shift) - 1));
+      for (int u = 0; u < U; ++u) cu_off[u] = ((uint32_t)(u * TPI) & bmask) * row_bytes;
+      // Keys s + u*TPI .. s + u*TPI + TPI - 1 lie in one block, at position
+      // (s & bmask) + ((u*TPI) & bmask) + g: s is a multiple of SUB, and the
+      // block size and SUB are powers of two with TPI <= block size. A load
+      // wholly past pool_end reads the last key's table entry and masks every
+      // lane. All table loads of a trip issue before the first use, so the trip
+      // waits for one scalar round trip.
+      auto issue = [&](int s, uint4* kr, uint4* vr, bool* ok) {
+        uint32_t raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) raw[u] = trow[min((uint32_t)(s + u * TPI), last_key) >> bs_shift];
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t trip_off = ((uint32_t)s & bmask) * row_bytes;
+        uint32_t voff[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const bool valid = raw[u] < (uint32_t)p.nb && g < pool_end - (s + u * TPI);
+          const uint32_t sb = raw[u] * blk_bytes + trip_off + cu_off[u];
+          voff[u] = (lane_off + sb) | (valid ? 0u : kBufOutOfRange);
+          ok[u] = valid;
         }
-        off[u] = valid ? row * row_bytes + col_bytes : kBufOutOfRange;
-        ok[u] = valid;
+#pragma unroll
+        for (int u = 0; u < U; ++u) kr[u] = load_buf(kres, voff[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) vr[u] = load_buf(vres, voff[u]);
+      };
+      // No load of this wave is waited for before its first K/V loads issue
+      // (the new key's row goes to LDS and is scored after the pool trips).
+      for (int s = s0; s < pool_end; s += kWaves * SUB) {
+        uint4 kr[U], vr[U];
+        bool ok[U];
+        issue(s, kr, vr, ok);
+        // Keep all 2*U loads in flight before the math: without this fence the
+        // scheduler may sink loads into the math to save registers, which
+        // serialises the memory latency.
+        __builtin_amdgcn_sched_barrier(0);
+        softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
       }
-      uint4 kr[U], vr[U];
+      if (one_new) score_new_key();
+    } else {
+      for (int s = s0; s < pool_end; s += kWaves * SUB) {
+        uint32_t off[U];
+        bool ok[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) kr[u] = load_buf(kres, off[u]);
+        for (int u = 0; u < U; ++u) {
+          const int t = s + u * TPI + g;
+          const bool valid = t < pool_end;
+          off[u] = valid ? (uint32_t)t * row_bytes + col_bytes : kBufOutOfRange;
+          ok[u] = valid;
+        }
+        uint4 kr[U], vr[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) vr[u] = load_buf(vres, off[u]);
-      // Keep all 2*U loads in flight before the math: without this fence the
-      // scheduler may sink loads into the math to save registers, which
-      // serialises the memory latency.
-      __builtin_amdgcn_sched_barrier(0);
-      softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
+        for (int u = 0; u < U; ++u) kr[u] = load_buf(kres, off[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) vr[u] = load_buf(vres, off[u]);
+        __builtin_amdgcn_sched_barrier(0);
+        softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
+      }
     }
   } else {
     for (int s = t_begin + wave * SUB; s < pool_end; s += kWaves * SUB) {
@@ -974,7 +1070,8 @@ void launch_attention(const AttnParams& p, hipStream_t stream) {
   const int64_t rh = (int64_t)p.batch * p.qlen * p.heads;
   const dim3 grid = p.grid3d ? dim3((uint32_t)p.heads, (uint32_t)(p.batch * p.qlen), (uint32_t)p.nchunk_max)
                              : dim3((uint32_t)rh, (uint32_t)p.nchunk_max);
-  const bool fast = p.kv_bytes <= kBufLimit && (!PAGED || p.bs_shift >= 0);
+  constexpr int kTpi = 64 / (D / Elt<DT>::EPL);  // keys per load instruction of a wave
+  const bool fast = p.kv_bytes <= kBufLimit && (!PAGED || (p.bs_shift >= 0 && (1 << p.bs_shift) >= kTpi));
   const uint32_t qlen_group = (uint32_t)p.qlen | ((uint32_t)p.group << 16);
   const uint32_t flags = (p.grid3d ? 1u : 0u) | (p.snake ? 2u : 0u) | (p.causal ? 4u : 0u) |
                          ((uint32_t)p.cu_shift << 8) | ((uint32_t)(p.bs_shift & 0xff) << 16);
