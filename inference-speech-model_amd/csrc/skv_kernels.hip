@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <type_traits>
 
 #include <stdarg.h>
 #include <stdint.h>
@@ -701,23 +702,18 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
   };
   const uint4 qv = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + j];
   // A fused append of one key (q_len 1, the decode step): the last wave loads
-  // the new K/V row here, with q, scores it and writes it to the pool, so the
-  // append adds no memory round trip. Its kn/vn address does not depend on the
-  // row length. The fast paged path loads it straight into LDS (no registers
-  // held across the pool loop) and scores it after its pool trips; the general
-  // path loads it into registers and scores it before the pool loop.
+  // the new K/V row, scores it and writes it to the pool, so the append adds no
+  // memory round trip. Its kn/vn address does not depend on the row length.
+  // The general path loads it here, into registers, and scores it before the
+  // pool loop; the fast paged path copies it into LDS at the start of the last
+  // wave's pool trips (no registers held across them) and scores it after them.
   const bool one_new = PAGED && p.kn && qlen == 1;
+  const int64_t new_off = (int64_t)b * p.nsb + (int64_t)kvh * p.nsh + j;
   uint4 nk = make_uint4(0u, 0u, 0u, 0u), nv = nk;
-  if (one_new && wave == kWaves - 1 && g == 0) {
-    const int64_t noff = (int64_t)b * p.nsb + (int64_t)kvh * p.nsh + j;
-    if constexpr (PAGED && FAST) {
-      using lds_ptr = __attribute__((address_space(3))) void*;
-      using glb_ptr = __attribute__((address_space(1))) void*;
-      __builtin_amdgcn_global_load_lds((glb_ptr)(p.kn + noff), (lds_ptr)&s_new[0][0], 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((glb_ptr)(p.vn + noff), (lds_ptr)&s_new[1][0], 16, 0, 0);
-    } else {
-      nk = p.kn[noff];
-      nv = p.vn[noff];
+  if constexpr (!(PAGED && FAST)) {
+    if (one_new && wave == kWaves - 1 && g == 0) {
+      nk = p.kn[new_off];
+      nv = p.vn[new_off];
     }
   }
 
@@ -851,19 +847,38 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
 #pragma unroll
         for (int u = 0; u < U; ++u) vr[u] = load_buf(vres, voff[u]);
       };
-      // No load of this wave is waited for before its first K/V loads issue
-      // (the new key's row goes to LDS and is scored after the pool trips).
-      for (int s = s0; s < pool_end; s += kWaves * SUB) {
-        uint4 kr[U], vr[U];
-        bool ok[U];
-        issue(s, kr, vr, ok);
-        // Keep all 2*U loads in flight before the math: without this fence the
-        // scheduler may sink loads into the math to save registers, which
-        // serialises the memory latency.
-        __builtin_amdgcn_sched_barrier(0);
-        softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
-      }
-      if (one_new) score_new_key();
+      // No load of this wave is waited for before its first K/V loads issue.
+      // The last wave's pool trips are a separate copy of the loop: while the
+      // LDS copy of the new key's row is outstanding, the compiler waits for
+      // all of a trip's loads before its first use, so only that copy carries
+      // it and the other waves' math starts on a trip's first load.
+      auto pool_trips = [&](auto last_wave) {
+        if constexpr (decltype(last_wave)::value) {
+          if (one_new && g == 0) {
+            using lds_ptr = __attribute__((address_space(3))) void*;
+            using glb_ptr = __attribute__((address_space(1))) void*;
+            __builtin_amdgcn_global_load_lds((glb_ptr)(p.kn + new_off), (lds_ptr)&s_new[0][0], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr)(p.vn + new_off), (lds_ptr)&s_new[1][0], 16, 0, 0);
+          }
+        }
+        for (int s = s0; s < pool_end; s += kWaves * SUB) {
+          uint4 kr[U], vr[U];
+          bool ok[U];
+          issue(s, kr, vr, ok);
+          // Keep all 2*U loads in flight before the math: without this fence
+          // the scheduler may sink loads into the math to save registers,
+          // which serialises the memory latency.
+          __builtin_amdgcn_sched_barrier(0);
+          softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
+        }
+        if constexpr (decltype(last_wave)::value) {
+          if (one_new) score_new_key();
+        }
+      };
+      if (__builtin_amdgcn_readfirstlane(wave) == kWaves - 1)
+        pool_trips(std::true_type{});
+      else
+        pool_trips(std::false_type{});
     } else {
       for (int s = s0; s < pool_end; s += kWaves * SUB) {
         uint32_t off[U];
