@@ -12,7 +12,8 @@ from HBM.
 
 Extra fields (same JSON line), Whisper-large-v3 decoder shapes (bf16, 20 heads
 x 64, batch 64):
-  large_v3_paged_attention  the same fused kernel at ctx U[1, 452]
+  large_v3_paged_attention  the same fused kernel at ctx U[1, 452] (and at batch 128,
+                            the large-v3 serving configuration's slot count)
   large_v3_cross_attention  attention over 1500 contiguous encoder positions
   large_v3_decode           end-to-end greedy decode through the scheduler's
                             captured graphs: 32 layers, d_model 1280, vocab
@@ -244,6 +245,17 @@ def large_v3_kernels(torch, native, dev, a):
             r["unsorted_rows_frac"] = round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
         del sets, fns
         torch.cuda.empty_cache()
+    # The same kernel at batch 128 (the large-v3 serving configuration's slot count).
+    sets = paged_sets(torch, native, dev, dt, 128, h, d, 16, 4096, 452, a.seed + 150, 0, True)
+    fns = [lambda s=s: native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, 0.125,
+                                              out=s.out, k_new=s.k_new, v_new=s.v_new) for s in sets]
+    avg = graph_launch_us(torch, fns)
+    byts = sum(s.bytes for s in sets) / len(sets)
+    out["large_v3_paged_attention"]["batch128"] = {
+        "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
+        "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del sets, fns
+    torch.cuda.empty_cache()
     t = 1500
     kvs = []
     for i in range(2):  # 2 x 491 MB > 256 MB last-level cache
