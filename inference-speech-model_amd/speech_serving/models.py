@@ -148,6 +148,22 @@ def add_norm(x: torch.Tensor, y: Optional[torch.Tensor], norm: nn.LayerNorm) -> 
     return s, norm(s)
 
 
+@torch.no_grad()
+def _init_normal(model: nn.Module, std: float, seed: int, draw_device: Optional[str]):
+    dev = torch.device(draw_device or "cpu")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    for m in model.modules():
+        if isinstance(m, (nn.Linear, nn.Conv1d, nn.Embedding)):
+            w = torch.empty(m.weight.shape, dtype=torch.float32, device=dev).normal_(0.0, std, generator=g)
+            m.weight.copy_(w.to(m.weight.dtype))
+            if getattr(m, "bias", None) is not None:
+                m.bias.zero_()
+        elif isinstance(m, nn.LayerNorm):
+            m.weight.fill_(1.0)
+            m.bias.zero_()
+    return model
+
+
 # ---------------------------------------------------------------------------
 # Layers.
 # ---------------------------------------------------------------------------
@@ -330,24 +346,12 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
         self.lm_head = nn.Linear(hidden_dim, vocab_size, bias=False)
 
     # -- initialisation used by the benchmark configs ------------------------------
-    @torch.no_grad()
     def init_normal_(self, std: float = 0.02, seed: int = 0,
                      draw_device: Optional[str] = None) -> "WhisperClassSpeechEncoderDecoderModel":
         """Weights of every Linear / Conv1d / Embedding ~ N(0, std), biases 0,
         LayerNorm 1 / 0. Draws are seeded on `draw_device` (default CPU, so every
         device gets the same values; a GPU draw is much faster for large models)."""
-        dev = torch.device(draw_device or "cpu")
-        g = torch.Generator(device=dev).manual_seed(seed)
-        for m in self.modules():
-            if isinstance(m, (nn.Linear, nn.Conv1d, nn.Embedding)):
-                w = torch.empty(m.weight.shape, dtype=torch.float32, device=dev).normal_(0.0, std, generator=g)
-                m.weight.copy_(w.to(m.weight.dtype))
-                if getattr(m, "bias", None) is not None:
-                    m.bias.zero_()
-            elif isinstance(m, nn.LayerNorm):
-                m.weight.fill_(1.0)
-                m.bias.zero_()
-        return self
+        return _init_normal(self, std, seed, draw_device)
 
     @property
     def dtype(self) -> torch.dtype:
@@ -453,3 +457,133 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
             x = layer._finish(x, True)
         logits = self.lm_head(self.decoder_norm(x[:, -1, :]))
         native.argmax(logits, out=g_output_tokens)
+
+
+# ---------------------------------------------------------------------------
+# Streaming multi-codebook TTS model (decoder-only, paged self-attention).
+# ---------------------------------------------------------------------------
+class MultiCodebookEmbedding(nn.Module):
+    """Sum of K per-codebook embeddings (reference models.py:23-51, same parameter names)."""
+
+    def __init__(self, num_codebooks: int, vocab_size: int, embed_dim: int):
+        super().__init__()
+        self.num_codebooks = num_codebooks
+        self.vocab_size = vocab_size
+        self.embed_dim = embed_dim
+        self.embeddings = nn.ModuleList([nn.Embedding(vocab_size, embed_dim) for _ in range(num_codebooks)])
+
+    def forward(self, input_codebooks: torch.Tensor) -> torch.Tensor:
+        """[B, S, K] codes -> [B, S, embed_dim]."""
+        if input_codebooks.shape[-1] != self.num_codebooks:
+            raise ValueError(f"Expected {self.num_codebooks} codebooks, got {input_codebooks.shape[-1]}")
+        x = self.embeddings[0](input_codebooks[..., 0])
+        for k in range(1, self.num_codebooks):
+            x = x + self.embeddings[k](input_codebooks[..., k])
+        return x
+
+
+class MultiCodebookHeads(nn.Module):
+    """One bias-free linear head per codebook (reference models.py:54-77, same parameter
+    names), computed as one GEMM over the concatenated head weights."""
+
+    def __init__(self, num_codebooks: int, hidden_dim: int, vocab_size: int):
+        super().__init__()
+        self.num_codebooks = num_codebooks
+        self.vocab_size = vocab_size
+        self.heads = nn.ModuleList([nn.Linear(hidden_dim, vocab_size, bias=False) for _ in range(num_codebooks)])
+        self._key = None
+        self._w: Optional[torch.Tensor] = None
+
+    def fused_weight(self) -> torch.Tensor:
+        """[K * V, hidden], rebuilt when any head weight changes."""
+        ws = tuple(h.weight for h in self.heads)
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
+        if key != self._key:
+            self._w = torch.cat([w.detach() for w in ws], dim=0).contiguous()
+            self._key = key
+        return self._w
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        """[B, S, hidden] -> logits [B, S, K, V]."""
+        b, s, _ = hidden_states.shape
+        return F.linear(hidden_states, self.fused_weight()).view(b, s, self.num_codebooks, self.vocab_size)
+
+
+class StreamingMultiCodebookTTSModel(nn.Module):
+    """Decoder-only model over K parallel codebook streams (reference models.py:211-295):
+    summed codebook embeddings, DecoderLayer stack (self-attention only, so each MLP
+    normalises with norm2), final LayerNorm, one head per codebook.
+
+    Entry points:
+        forward(input_codebooks, past_key_values, use_cache)  the reference signature,
+            contiguous past K/V ([B, H, T, D] per layer) -> logits [B, S, K, V] + cache
+        decode_step_paged(input_codebooks, PagedKV)  the paged hot path: per layer one
+            fused launch appends the new frames' K/V through the block table and attends
+    """
+
+    def __init__(self, num_layers: int = 4, num_heads: int = 4, hidden_dim: int = 256, num_codebooks: int = 4,
+                 vocab_size: int = 1024):
+        super().__init__()
+        self.num_layers = num_layers
+        self.num_heads = num_heads
+        self.head_dim = hidden_dim // num_heads
+        self.hidden_dim = hidden_dim
+        self.num_codebooks = num_codebooks
+        self.vocab_size = vocab_size
+
+        class Config:
+            pass
+
+        self.config = Config()
+        self.config.num_hidden_layers = num_layers
+        self.config.num_attention_heads = num_heads
+        self.config.num_key_value_heads = num_heads
+        self.config.hidden_size = hidden_dim
+        self.config.vocab_size = vocab_size
+
+        self.embeddings = MultiCodebookEmbedding(num_codebooks, vocab_size, hidden_dim)
+        self.layers = nn.ModuleList(
+            [DecoderLayer(hidden_dim, num_heads, self.head_dim, is_decoder=True) for _ in range(num_layers)])
+        self.norm = nn.LayerNorm(hidden_dim)
+        self.heads = MultiCodebookHeads(num_codebooks, hidden_dim, vocab_size)
+
+    def init_normal_(self, std: float = 0.02, seed: int = 0,
+                     draw_device: Optional[str] = None) -> "StreamingMultiCodebookTTSModel":
+        """Weights of every Linear / Embedding ~ N(0, std), LayerNorm 1 / 0 (seeded)."""
+        return _init_normal(self, std, seed, draw_device)
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self.norm.weight.dtype
+
+    def forward(self, input_codebooks: torch.Tensor, past_key_values: Optional[Any] = None,
+                use_cache: bool = True) -> ModelOutput:
+        x = self.embeddings(input_codebooks)
+        cache = KVCache() if use_cache else None
+        for i, layer in enumerate(self.layers):
+            past = None
+            if past_key_values is not None:
+                if hasattr(past_key_values, "layers"):
+                    if i < len(past_key_values.layers):
+                        past = (past_key_values.layers[i].keys, past_key_values.layers[i].values)
+                elif isinstance(past_key_values, (list, tuple)) and i < len(past_key_values):
+                    past = past_key_values[i]
+            x, new_kv, _ = layer(x, past_key_values=past)
+            if use_cache:
+                cache.layers.append(LayerKV(new_kv[0], new_kv[1]))
+        return ModelOutput(self.heads(self.norm(x)), cache)
+
+    def decode_step_paged(self, input_codebooks: torch.Tensor, kv: PagedKV, last_only: bool = True) -> torch.Tensor:
+        """Run the model on input_codebooks [B, Q, K] whose K/V go into the paged pool at
+        positions ctx_lens-Q .. ctx_lens-1 (causal among the Q frames); returns the logits
+        of the last frame [B, K, V] (or of every frame, [B, Q, K, V])."""
+        x = self.embeddings(input_codebooks)
+        pending = None
+        for l, layer in enumerate(self.layers):
+            x, pending = layer.forward_paged(x, l, kv, None, pending)
+        if last_only:
+            x = x[:, -1:]
+            pending = None if pending is None else pending[:, -1:]
+        _, h = add_norm(x, pending, self.norm)
+        logits = self.heads(h)
+        return logits[:, 0] if last_only else logits

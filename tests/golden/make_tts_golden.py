@@ -1,0 +1,119 @@
+"""Write golden vectors of the reference's streaming multi-codebook TTS model and engine.
+
+Run in the development container, where the reference repository is mounted:
+    python tests/golden/make_tts_golden.py [/path/to/reference]
+It imports speech_serving.models.StreamingMultiCodebookTTSModel and
+speech_serving.tts_engine.StreamingTTSEngine from the reference (CPU,
+float32), builds a small seeded model with the shapes of the reference's own
+TTS test (test_speech_engine.py:35-91), and saves to
+tests/golden/tts_small_golden.npz (numpy arrays only, no pickles):
+    param.*                 the model's state_dict
+    prompts                 [R, P, K] int64 prompt codebook frames
+    prefill_logits{r}       model(prompt r) logits [1, P, K, V]
+    prefill_k{l}/v{l}       request 0's prefill K/V per layer [1, H, P, D]
+    step_logits{r}          the last-position logits of every generated frame
+                            of request r, from the model run incrementally
+                            with its contiguous past [F, K, V]
+    engine_frames{r}        the reference engine's frames for request r [F, K]
+    engine_blocks           allocated / free block counts after the run
+The oracle (oracle/tts.py) is checked against this file by
+tests/test_tts_oracle.py, and the HIP engine by tests/test_tts_gpu.py.
+Nothing on the GPU box reads the reference.
+"""
+import json
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+OUT = os.path.join(HERE, "tts_small_golden.npz")
+
+CONFIG = dict(num_layers=2, num_heads=4, hidden_dim=64, num_codebooks=4, vocab_size=128)
+BLOCK_SIZE = 8
+NUM_BLOCKS = 32
+MAX_BATCH = 2
+REQUESTS = 3
+PROMPT_LEN = 10
+FRAMES = 15
+MIN_MARGIN = 1e-3  # smallest top-1 minus top-2 logit gap the chosen seed must keep
+
+
+def build(seed, TTSModel):
+    torch.manual_seed(seed)
+    model = TTSModel(**CONFIG).eval()
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        # Distinct LayerNorm parameters so norm1 / norm2 / final norm are distinguishable.
+        for mod in model.modules():
+            if isinstance(mod, torch.nn.LayerNorm):
+                mod.weight.add_(0.2 * torch.randn(mod.weight.shape, generator=g))
+                mod.bias.add_(0.2 * torch.randn(mod.bias.shape, generator=g))
+    prompts = torch.randint(0, CONFIG["vocab_size"], (REQUESTS, PROMPT_LEN, CONFIG["num_codebooks"]), generator=g)
+    return model, prompts
+
+
+def incremental(model, prompt, frames):
+    """Prefill, then one frame per step with the contiguous past: last-position logits per frame."""
+    out = model(input_codebooks=prompt[None], use_cache=True)
+    logits = []
+    for _ in range(frames):
+        last = out.logits[0, -1]  # [K, V]
+        logits.append(last.clone())
+        nxt = torch.argmax(last, dim=-1)[None, None]  # [1, 1, K]
+        out = model(input_codebooks=nxt, past_key_values=out.past_key_values, use_cache=True)
+    return torch.stack(logits)
+
+
+def main(ref_root: str) -> None:
+    sys.path.insert(0, ref_root)
+    from speech_serving.models import StreamingMultiCodebookTTSModel  # noqa: E402  (reference)
+    from speech_serving.tts_engine import StreamingTTSEngine  # noqa: E402  (reference)
+    from paged_kv_cache.block_manager import BlockManager  # noqa: E402  (reference)
+
+    for seed in range(2024, 2124):
+        model, prompts = build(seed, StreamingMultiCodebookTTSModel)
+        with torch.no_grad():
+            steps = [incremental(model, prompts[r], FRAMES) for r in range(REQUESTS)]
+        top2 = torch.stack(steps).topk(2, dim=-1).values
+        margin = float((top2[..., 0] - top2[..., 1]).min())
+        if margin >= MIN_MARGIN:
+            break
+    else:
+        raise SystemExit("no seed in range keeps every greedy margin above MIN_MARGIN")
+
+    out = {f"param.{k}": v.detach().numpy().copy() for k, v in model.state_dict().items()}
+    out["prompts"] = prompts.numpy().astype(np.int64)
+    with torch.no_grad():
+        for r in range(REQUESTS):
+            pre = model(input_codebooks=prompts[r][None], use_cache=True)
+            out[f"prefill_logits{r}"] = pre.logits.numpy()
+            if r == 0:
+                for l in range(CONFIG["num_layers"]):
+                    out[f"prefill_k{l}"] = pre.past_key_values.layers[l].keys.numpy()
+                    out[f"prefill_v{l}"] = pre.past_key_values.layers[l].values.numpy()
+            out[f"step_logits{r}"] = steps[r].numpy()
+
+        bm = BlockManager(num_layers=CONFIG["num_layers"], num_kv_heads=CONFIG["num_heads"],
+                          head_dim=CONFIG["hidden_dim"] // CONFIG["num_heads"], block_size=BLOCK_SIZE,
+                          num_blocks=NUM_BLOCKS, dtype=torch.float32, device="cpu")
+        engine = StreamingTTSEngine(model, bm, max_batch_size=MAX_BATCH, device="cpu")
+        for r in range(REQUESTS):
+            engine.submit(prompts[r], max_new_frames=FRAMES)
+        done = sorted(engine.run_until_done(), key=lambda q: q.id)
+    for q in done:
+        frames = torch.stack(q.generated_frames).numpy().astype(np.int64)
+        out[f"engine_frames{q.id}"] = frames
+        # The engine's frames are the argmax of the incremental model's logits.
+        assert (frames == steps[q.id].argmax(-1).numpy()).all(), f"engine and incremental model differ (req {q.id})"
+    out["engine_blocks"] = np.array([bm.allocated_block_count, bm.num_free_blocks], dtype=np.int64)
+    out["config_json"] = np.frombuffer(json.dumps(dict(
+        CONFIG, seed=seed, block_size=BLOCK_SIZE, num_blocks=NUM_BLOCKS, max_batch=MAX_BATCH,
+        requests=REQUESTS, prompt_len=PROMPT_LEN, frames=FRAMES, min_margin=margin)).encode(), dtype=np.uint8)
+    np.savez_compressed(OUT, **out)
+    print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(out)} arrays), seed {seed}, min margin {margin:.4g}")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -1,0 +1,171 @@
+"""StreamingTTSEngine / StreamingMultiCodebookTTSModel on the paged kernels.
+
+- The reference's own TTS test (test_speech_engine.py:35-91), unchanged in substance.
+- Parity with the reference: the golden file tests/golden/tts_small_golden.npz (written from
+  the reference model and engine, CPU float32) holds the weights, prompts, prefill logits and
+  K/V, the logits of every generated frame and the engine's frames. Here the same weights run
+  in float32 on the GPU: frames must be identical, logits within 1e-4 (the golden seed keeps
+  every greedy margin above 2.7e-3), the prefill K/V written into the pool within 1e-5.
+- Bookkeeping: every request's block table after each frame equals the oracle engine's
+  (oracle/tts.py, LIFO free list), all blocks return to the pool.
+- Failure paths: a raising frame callback only warns; running out of blocks mid-decode ends
+  that request alone.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.tts import Engine
+from speech_serving import BlockManager, StreamingMultiCodebookTTSModel, StreamingTTSEngine
+from speech_serving.models import PagedKV
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "tts_small_golden.npz")
+
+
+def _golden(device):
+    z = np.load(GOLDEN)
+    cfg = json.loads(bytes(z["config_json"]).decode())
+    model = StreamingMultiCodebookTTSModel(cfg["num_layers"], cfg["num_heads"], cfg["hidden_dim"],
+                                           cfg["num_codebooks"], cfg["vocab_size"])
+    state = {k[len("param."):]: torch.from_numpy(z[k]) for k in z.files if k.startswith("param.")}
+    model.load_state_dict(state, strict=True)
+    return z, cfg, model.to(device=device, dtype=torch.float32).eval()
+
+
+def _bm(cfg, device, dtype=torch.float32, num_blocks=None):
+    return BlockManager(num_layers=cfg["num_layers"], num_kv_heads=cfg["num_heads"],
+                        head_dim=cfg["hidden_dim"] // cfg["num_heads"], block_size=cfg["block_size"],
+                        num_blocks=num_blocks or cfg["num_blocks"], dtype=dtype, device=str(device))
+
+
+def test_reference_streaming_tts_engine(cuda):
+    """test_speech_engine.py:35-91: 3 requests x 15 frames, batch 2, block size 8, 32 blocks, fp16."""
+    num_layers, num_heads, hidden_dim, num_codebooks, vocab_size, block_size = 2, 4, 64, 4, 128, 8
+    torch.manual_seed(0)
+    model = StreamingMultiCodebookTTSModel(num_layers=num_layers, num_heads=num_heads, hidden_dim=hidden_dim,
+                                           num_codebooks=num_codebooks, vocab_size=vocab_size)
+    model = model.to(device=cuda, dtype=torch.float16).eval()
+    bm = BlockManager(num_layers=num_layers, num_kv_heads=num_heads, head_dim=hidden_dim // num_heads,
+                      block_size=block_size, num_blocks=32, dtype=torch.float16, device=str(cuda))
+    engine = StreamingTTSEngine(model, bm, max_batch_size=2, device=str(cuda))
+    frames_received = {}
+
+    def callback_factory(req_id):
+        def cb(rid, frame):
+            assert rid == req_id and frame.shape == (num_codebooks,) and frame.dtype == torch.int64
+            frames_received[rid] = frames_received.get(rid, 0) + 1
+        return cb
+
+    for i in range(3):
+        prompt = torch.randint(0, vocab_size, (10, num_codebooks), device=cuda)
+        engine.submit(prompt, max_new_frames=15, on_frame_callback=callback_factory(i))
+    completed = engine.run_until_done()
+
+    assert len(completed) == 3
+    for req in completed:
+        assert req.done
+        assert req.generated_count == 15
+        assert len(req.generated_frames) == 15
+        assert req.generated_frames[0].shape[0] == num_codebooks
+        assert all(int(f.min()) >= 0 and int(f.max()) < vocab_size for f in req.generated_frames)
+    assert frames_received == {0: 15, 1: 15, 2: 15}
+    assert bm.allocated_block_count == 0
+    assert bm.num_free_blocks == 32
+
+
+def test_frames_match_reference_engine(cuda):
+    z, cfg, model = _golden(cuda)
+    bm = _bm(cfg, cuda)
+    engine = StreamingTTSEngine(model, bm, max_batch_size=cfg["max_batch"], device=str(cuda))
+    tables = {}
+    emit = engine._emit
+
+    def record(req, frame):
+        tables.setdefault(req.id, []).append(list(req.block_table))
+        return emit(req, frame)
+
+    engine._emit = record
+    for r in range(cfg["requests"]):
+        engine.submit(torch.from_numpy(z["prompts"][r]), max_new_frames=cfg["frames"])
+    done = engine.run_until_done()
+    assert [q.id for q in done] == [0, 1, 2]
+    for q in done:
+        got = torch.stack(q.generated_frames).cpu().numpy()
+        assert np.array_equal(got, z[f"engine_frames{q.id}"]), q.id
+    assert [bm.allocated_block_count, bm.num_free_blocks] == z["engine_blocks"].tolist()
+    _, history, _ = Engine(cfg["num_blocks"], cfg["block_size"], cfg["max_batch"]).run(
+        [cfg["prompt_len"]] * cfg["requests"], [cfg["frames"]] * cfg["requests"])
+    assert tables == history
+
+
+def test_prefill_and_step_logits_match_reference(cuda):
+    z, cfg, model = _golden(cuda)
+    bm = _bm(cfg, cuda)
+    bs = cfg["block_size"]
+    for r in range(cfg["requests"]):
+        prompt = torch.from_numpy(z["prompts"][r]).to(cuda)
+        p = prompt.shape[0]
+        blocks = [bm.allocate_block() for _ in range(-(-(p + cfg["frames"]) // bs))]
+        table = torch.tensor([blocks], dtype=torch.int32, device=cuda)
+
+        def kv(n):
+            return PagedKV(bm.key_pool, bm.value_pool, table, torch.tensor([n], dtype=torch.int32, device=cuda), n)
+
+        with torch.no_grad():
+            logits = model.decode_step_paged(prompt[None], kv(p), last_only=False)  # [1, P, K, V]
+            np.testing.assert_allclose(logits.cpu().numpy(), z[f"prefill_logits{r}"], atol=1e-4, rtol=0)
+            if r == 0:
+                for l in range(cfg["num_layers"]):
+                    for pool, key in ((bm.key_pool[l], "prefill_k"), (bm.value_pool[l], "prefill_v")):
+                        got = pool[blocks].reshape(-1, cfg["num_heads"], pool.shape[-1])[:p].permute(1, 0, 2)
+                        np.testing.assert_allclose(got.cpu().numpy(), z[f"{key}{l}"][0], atol=1e-5, rtol=0)
+            want = z[f"step_logits{r}"]
+            last = logits[:, -1]
+            n = p
+            for f in range(cfg["frames"]):
+                np.testing.assert_allclose(last[0].cpu().numpy(), want[f], atol=1e-4, rtol=0, err_msg=f"r{r} f{f}")
+                nxt = last.argmax(-1)[:, None, :]  # [1, 1, K]
+                n += 1
+                last = model.decode_step_paged(nxt, kv(n))
+        bm.free_blocks(blocks)
+    assert bm.allocated_block_count == 0
+
+
+def test_raising_callback_only_warns(cuda, capsys):
+    z, cfg, model = _golden(cuda)
+    bm = _bm(cfg, cuda)
+    engine = StreamingTTSEngine(model, bm, max_batch_size=2, device=str(cuda))
+
+    def bad(rid, frame):
+        raise ValueError("listener gone")
+
+    engine.submit(torch.from_numpy(z["prompts"][0]), max_new_frames=4, on_frame_callback=bad)
+    done = engine.run_until_done()
+    assert len(done) == 1 and done[0].generated_count == 4
+    assert np.array_equal(torch.stack(done[0].generated_frames).cpu().numpy(), z["engine_frames0"][:4])
+    assert "Exception in frame callback" in capsys.readouterr().out
+    assert bm.allocated_block_count == 0
+
+
+def test_out_of_blocks_mid_decode_ends_that_request(cuda, capsys):
+    """4 blocks of 8: two 10-frame prompts take 2 blocks each; the first to need a third block
+    (sequence length 16) fails and is released, after which the other one continues."""
+    z, cfg, model = _golden(cuda)
+    bm = _bm(cfg, cuda, num_blocks=4)
+    engine = StreamingTTSEngine(model, bm, max_batch_size=2, device=str(cuda))
+    for r in range(2):
+        engine.submit(torch.from_numpy(z["prompts"][r]), max_new_frames=cfg["frames"])
+    done = engine.run_until_done()
+    out = capsys.readouterr().out
+    assert "Error executing step for TTS request 0" in out
+    assert [q.id for q in done] == [0, 1]
+    assert done[0].generated_count == 7  # frames 1..7 at sequence lengths 10..16, the 8th needs block 3
+    assert done[1].generated_count == cfg["frames"]
+    assert np.array_equal(torch.stack(done[1].generated_frames).cpu().numpy(), z["engine_frames1"])
+    assert np.array_equal(torch.stack(done[0].generated_frames).cpu().numpy(), z["engine_frames0"][:7])
+    assert bm.allocated_block_count == 0 and bm.num_free_blocks == 4
