@@ -15,6 +15,8 @@ x 64, batch 64):
   large_v3_paged_attention  the same fused kernel at ctx U[1, 452] (and at batch 128,
                             the large-v3 serving configuration's slot count)
   large_v3_cross_attention  attention over 1500 contiguous encoder positions
+  tts_decode                the streaming multi-codebook TTS engine (reference TTS
+                            model's default shape, 64 requests x 256 frames)
   large_v3_decode           end-to-end greedy decode through the scheduler's
                             captured graphs: 32 layers, d_model 1280, vocab
                             51866, N(0, 0.02) weights, 64 requests x 448 tokens,
@@ -57,12 +59,13 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-large-v3", action="store_true", help="skip the large-v3 kernel and decode measurements")
     ap.add_argument("--no-decode", action="store_true", help="skip the large-v3 decode (keep its kernel measurements)")
+    ap.add_argument("--no-tts", action="store_true", help="skip the streaming TTS engine measurement")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--decode-tokens", type=int, default=448)
     ap.add_argument("--decode-layers", type=int, default=32)
-    ap.add_argument("--mode", choices=["attention", "copy", "decode"], default="attention",
+    ap.add_argument("--mode", choices=["attention", "copy", "decode", "tts"], default="attention",
                     help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling; "
-                         "decode: only the large-v3-shaped greedy decode")
+                         "decode: only the large-v3-shaped greedy decode; tts: only the streaming TTS engine")
     ap.add_argument("--copy-mib", type=int, default=512)
     return ap.parse_args()
 
@@ -324,6 +327,53 @@ def large_v3_decode(torch, dev, a):
     return res
 
 
+def tts_decode(torch, dev, a):
+    """Streaming multi-codebook TTS on the paged engine: the reference TTS model's default shape
+    (4 layers, 4 heads x 64, 4 codebooks, vocab 1024), bf16, 64 concurrent requests with
+    32-frame prompts, 256 frames each, block size 16. Admission (prompt prefill of all 64
+    requests and their first frame) is timed apart from the steady decode."""
+    from speech_serving import BlockManager, StreamingMultiCodebookTTSModel, StreamingTTSEngine
+
+    layers, heads, hidden, books, vocab, bs = 4, 4, 256, 4, 1024, 16
+    batch, prompt_len, frames = 64, 32, 256
+    model = StreamingMultiCodebookTTSModel(layers, heads, hidden, books, vocab).init_normal_(0.02, seed=a.seed)
+    model = model.to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(a.seed + 7)
+
+    def engine_for(n, f):
+        bm = BlockManager(layers, heads, hidden // heads, bs, num_blocks=n * math.ceil((prompt_len + f) / bs),
+                          dtype=torch.bfloat16, device=str(dev))
+        eng = StreamingTTSEngine(model, bm, max_batch_size=n, device=str(dev))
+        for _ in range(n):
+            eng.submit(torch.randint(0, vocab, (prompt_len, books), generator=g), max_new_frames=f)
+        return eng, bm
+
+    eng, _ = engine_for(4, 8)  # warm-up
+    eng.run_until_done()
+    eng, bm = engine_for(batch, frames)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.step()  # admission: 64 prefills + first frames, then one decode step
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    steps = 0
+    while eng.active or eng.queue:
+        eng.step()
+        steps += 1
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    done = eng.completed
+    ok = len(done) == batch and all(q.generated_count == frames for q in done) and bm.allocated_block_count == 0
+    decoded = batch * steps
+    return {"workload": f"StreamingTTSEngine, bf16, {layers} layers, d_model {hidden}, {heads} heads x "
+                        f"{hidden // heads}, {books} codebooks x vocab {vocab}, {batch} requests x {frames} frames "
+                        f"from {prompt_len}-frame prompts, block size {bs}",
+            "decode_frames_per_s": round(decoded / (t2 - t1), 1),
+            "decode_codebook_tokens_per_s": round(decoded * books / (t2 - t1), 1),
+            "ms_per_decode_step": round((t2 - t1) / steps * 1e3, 3), "decode_steps": steps,
+            "admission_s": round(t1 - t0, 3), "completed_ok": ok}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -343,6 +393,10 @@ def main():
     if a.mode == "decode":  # the large-v3-shaped greedy decode alone (for kernel traces of the decode step)
         native.lib()
         print(json.dumps({"large_v3_decode": large_v3_decode(torch, dev, a)}))
+        return
+    if a.mode == "tts":  # the streaming TTS engine alone
+        native.lib()
+        print(json.dumps({"tts_decode": tts_decode(torch, dev, a)}))
         return
     dtype = torch.float16
     scale = 1.0 / math.sqrt(a.head_dim)
@@ -459,6 +513,8 @@ def main():
         result.update(large_v3_kernels(torch, native, dev, a))
         if not a.no_decode:
             result["large_v3_decode"] = large_v3_decode(torch, dev, a)
+    if not a.no_tts:
+        result["tts_decode"] = tts_decode(torch, dev, a)
     print(json.dumps(result), flush=True)
 
 
