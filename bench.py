@@ -365,13 +365,43 @@ def tts_decode(torch, dev, a):
     done = eng.completed
     ok = len(done) == batch and all(q.generated_count == frames for q in done) and bm.allocated_block_count == 0
     decoded = batch * steps
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = tts_cpu_baseline(model, prompt_len, books, vocab, a.seed, 3.0)
     return {"workload": f"StreamingTTSEngine, bf16, {layers} layers, d_model {hidden}, {heads} heads x "
                         f"{hidden // heads}, {books} codebooks x vocab {vocab}, {batch} requests x {frames} frames "
                         f"from {prompt_len}-frame prompts, block size {bs}",
             "decode_frames_per_s": round(decoded / (t2 - t1), 1),
             "decode_codebook_tokens_per_s": round(decoded * books / (t2 - t1), 1),
             "ms_per_decode_step": round((t2 - t1) / steps * 1e3, 3), "decode_steps": steps,
-            "admission_s": round(t1 - t0, 3), "completed_ok": ok}
+            "admission_s": round(t1 - t0, 3), "completed_ok": ok, "cpu_baseline": cpu}
+
+
+def tts_cpu_baseline(model, prompt_len, books, vocab, seed, budget_s):
+    """The numpy oracle of the TTS model (float64, one thread) decoding one request frame by frame
+    with its contiguous past, as the reference engine does per request: frames/s."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle.tts import TTSModel
+
+    state = {k: v.float().cpu().numpy() for k, v in model.state_dict().items()}
+    m = TTSModel(state, model.num_heads, model.head_dim)
+    prompt = np.random.default_rng(seed).integers(0, vocab, (prompt_len, books))
+    frames = 0
+    with threadpool_limits(limits=1):
+        logits, past = m.forward(prompt[None])
+        t0 = time.perf_counter()
+        while True:
+            tok = logits[0, -1].argmax(axis=-1)
+            logits, past = m.forward(tok[None, None], past)
+            frames += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+    return {"value": round(frames / el, 2), "unit": "frames/s", "cores": 1, "kind": "port",
+            "sample": f"{frames} decode frames of one request (context {prompt_len}..{prompt_len + frames}) "
+                      f"by the numpy oracle"}
 
 
 def main():
