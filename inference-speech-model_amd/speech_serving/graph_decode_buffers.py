@@ -159,6 +159,7 @@ class GraphDecodeBuffers:
 
         self.graphs: Dict[int, torch.cuda.CUDAGraph] = {}
         self._graph_pool = None
+        self._graph_workspace: Optional[torch.Tensor] = None
         if capture:
             self.capture_all_buckets()
 
@@ -279,6 +280,9 @@ class GraphDecodeBuffers:
                 if self._graph_pool is None:
                     self._graph_pool = g.pool()
                 self.graphs[b] = g
+        # The graphs hold the attention workspace's address: keep that buffer alive even if a
+        # later, larger eager call grows the device's workspace (which drops the old one).
+        self._graph_workspace = native.reserve_workspace(0, self.device)
         torch.cuda.synchronize(self.device)
 
     # ------------------------------------------------------------------ stepping

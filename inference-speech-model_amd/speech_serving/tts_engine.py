@@ -17,12 +17,22 @@ paged kernel's multi-token append with the causal mask).
 Bookkeeping is the reference's: ceil(prompt_len / block_size) blocks at admission,
 one more whenever the sequence length reaches a block boundary before a step,
 all of a request's blocks freed when it completes or fails.
+
+graph_decode (default on): each active request keeps a fixed slot; the decode step
+of a batch bucket (the smallest of 1, 2, 4, ... covering the highest busy slot)
+is captured once in a HIP graph over static per-slot buffers (input frame, block
+table, length, output tokens) and replayed every step: the graph runs the layers,
+the argmax into the slot tokens and the copy of those tokens into the next step's
+input frames, so a step's host work is two small uploads (lengths, changed table
+rows) and one replay. Idle slots have length 0: their attention launches return
+at once and append nothing. The context cap of the captured graphs doubles when a
+request outgrows it (the graphs are captured again).
 """
 from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
-from typing import Callable, List, Optional
+from typing import Callable, Dict, List, Optional
 
 import torch
 
@@ -55,16 +65,25 @@ class StreamingTTSEngine:
     """Continuous batching of streaming multi-codebook TTS requests over a paged KV pool."""
 
     def __init__(self, model: StreamingMultiCodebookTTSModel, block_manager: BlockManager, max_batch_size: int = 8,
-                 device: str = "cuda"):
+                 device: str = "cuda", graph_decode: bool = True):
         self.model = model
         self.block_manager = block_manager
         self.max_batch_size = max_batch_size
         self.device = device
+        self.graph_decode = graph_decode
 
         self.active: List[TTSRequest] = []
         self.queue: List[TTSRequest] = []
         self.completed: List[TTSRequest] = []
         self._next_id = 0
+
+        # graph decode state (allocated on first use)
+        self._slot_of: Dict[int, int] = {}  # request id -> slot
+        self._free_slots = list(range(max_batch_size))
+        self._cap = 0  # context cap (tokens) of the captured graphs and the table width
+        self._graphs: Dict[int, torch.cuda.CUDAGraph] = {}
+        self._graph_pool = None
+        self._graph_workspaces: List[torch.Tensor] = []  # attention workspaces the graphs were captured with
 
     # -- API -------------------------------------------------------------------
     def submit(self, prompt_codebooks: torch.Tensor, max_new_frames: int = 100, arrival_time: float = 0.0,
@@ -94,7 +113,11 @@ class StreamingTTSEngine:
         still_active: List[TTSRequest] = []
         if batch:
             try:
-                frames = self._decode(batch)
+                if self.graph_decode:
+                    by_id = self._decode_graph(batch)
+                    frames = [by_id[r.id] for r in batch]
+                else:
+                    frames = self._decode(batch)
             except Exception as e:
                 for req in batch:
                     self._fail(req, e)
@@ -135,6 +158,8 @@ class StreamingTTSEngine:
                 raise
             req.first_token_time = time.perf_counter()
             if self._emit(req, frame):
+                if self.graph_decode:
+                    self._take_slot(req, frame)
                 self.active.append(req)
 
     def _paged_kv(self, tables: List[List[int]], ctx: List[int]) -> PagedKV:
@@ -164,6 +189,128 @@ class StreamingTTSEngine:
         b, k, v = logits.shape
         return native.argmax(logits.reshape(b * k, v)).view(b, k)
 
+    # -- graph decode ------------------------------------------------------------
+    def _buckets(self) -> List[int]:
+        out, b = [], 1
+        while b < self.max_batch_size:
+            out.append(b)
+            b *= 2
+        return out + [self.max_batch_size]
+
+    def _setup_graph_buffers(self, cap: int) -> None:
+        """(Re)allocate the static slot buffers for a context cap; drops captured graphs."""
+        bm = self.block_manager
+        s, k = self.max_batch_size, self.model.num_codebooks
+        width = -(-cap // bm.block_size)
+        dev = bm.key_pool[0].device
+        if self._graphs:
+            torch.cuda.synchronize(dev)  # no replay of the graphs being dropped is still pending
+        self._graphs.clear()
+        self._graph_pool = None
+        self._cap = width * bm.block_size
+        self._width = width
+        self.g_inputs = torch.zeros((s, 1, k), dtype=torch.int64, device=dev)
+        # Per-slot metadata in one buffer (one upload per step): lengths [S], then tables [S, W].
+        self.g_meta = torch.zeros(s + s * width, dtype=torch.int32, device=dev)
+        self.g_ctx = self.g_meta[:s]
+        self.g_tables = self.g_meta[s:].view(s, width)
+        self.g_tokens = torch.zeros(s * k, dtype=torch.int64, device=dev)
+        # Two pinned banks, each reused only after its previous upload has run; each bank
+        # tracks how many table entries of every slot it holds.
+        self._banks = [torch.zeros(s + s * width, dtype=torch.int32).pin_memory() for _ in range(2)]
+        self._bank_events = [None, None]
+        self._bank_filled = [[-1] * s, [-1] * s]
+        self._bank_i = 0
+        for r in self.active:
+            self.g_inputs[self._slot_of[r.id]].copy_(r.last_frame_codebooks[0])
+        self._graph_workspaces = []
+        for b in self._buckets():
+            native.reserve_attention(b, self.model.num_heads, self.model.head_dim, self._cap, self.model.dtype, dev)
+
+    def _graph_step(self, inputs, tables, ctx, tokens, b: int) -> None:
+        """The captured decode step of bucket b over the given slot buffers."""
+        bm = self.block_manager
+        k, v = self.model.num_codebooks, self.model.vocab_size
+        kv = PagedKV(bm.key_pool, bm.value_pool, tables[:b], ctx[:b], self._cap)
+        logits = self.model.decode_step_paged(inputs[:b], kv)  # [b, K, V]
+        native.argmax(logits.reshape(b * k, v), out=tokens[:b * k])
+        inputs[:b, 0].copy_(tokens[:b * k].view(b, k))
+
+    def _graph_for(self, b: int) -> torch.cuda.CUDAGraph:
+        g = self._graphs.get(b)
+        if g is not None:
+            return g
+        dev = self.g_inputs.device
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.no_grad(), torch.cuda.stream(side):
+            # Warm-up on throwaway buffers (all lengths 0, so nothing is appended): builds the
+            # model's fused weights and the GEMM library state outside the capture.
+            scratch = (torch.zeros_like(self.g_inputs), torch.zeros_like(self.g_tables),
+                       torch.zeros_like(self.g_ctx), torch.zeros_like(self.g_tokens))
+            self._graph_step(*scratch, b)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        kwargs = {"pool": self._graph_pool} if self._graph_pool is not None else {}
+        with torch.no_grad(), torch.cuda.graph(g, stream=side, **kwargs):
+            self._graph_step(self.g_inputs, self.g_tables, self.g_ctx, self.g_tokens, b)
+        if self._graph_pool is None:
+            self._graph_pool = g.pool()
+        self._graphs[b] = g
+        # The graph holds the attention workspace's address: keep that buffer alive even if a
+        # later, larger call grows the device's workspace (which drops the old one).
+        ws = native.reserve_workspace(0, dev)
+        if all(w.data_ptr() != ws.data_ptr() for w in self._graph_workspaces):
+            self._graph_workspaces.append(ws)
+        return g
+
+    def _decode_graph(self, batch: List[TTSRequest]) -> Dict[int, torch.Tensor]:
+        """One frame for every request of the batch via the captured step; request id -> [K] frame."""
+        need = max(r.seq_len + 1 for r in batch)
+        if need > self._cap:
+            cap = max(256, self._cap)
+            while cap < need:
+                cap *= 2
+            self._setup_graph_buffers(cap)
+        top = max(self._slot_of[r.id] for r in batch) + 1
+        b = next(x for x in self._buckets() if x >= top)
+        i = self._bank_i
+        self._bank_i ^= 1
+        if self._bank_events[i] is not None:
+            self._bank_events[i].synchronize()
+        bank, filled, s = self._banks[i], self._bank_filled[i], self.max_batch_size
+        host = bank.numpy()
+        host[:s] = 0
+        tables = host[s:].reshape(s, self._width)
+        for r in batch:
+            slot = self._slot_of[r.id]
+            host[slot] = r.seq_len + 1
+            n = len(r.block_table)
+            if filled[slot] != n:
+                tables[slot, :n] = r.block_table
+                filled[slot] = n
+        self.g_meta.copy_(bank, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._bank_events[i] = ev
+        self._graph_for(b).replay()
+        step = self.g_tokens[:b * self.model.num_codebooks].view(b, -1).clone()
+        return {r.id: step[self._slot_of[r.id]] for r in batch}
+
+    def _take_slot(self, req: TTSRequest, frame: torch.Tensor) -> None:
+        slot = self._free_slots.pop(0)
+        self._slot_of[req.id] = slot
+        if self._cap:
+            for filled in self._bank_filled:
+                filled[slot] = -1  # a new request's table: every bank rewrites the row
+            self.g_inputs[slot, 0].copy_(frame)
+
+    def _release_slot(self, req: TTSRequest) -> None:
+        slot = self._slot_of.pop(req.id, None)
+        if slot is not None:
+            self._free_slots.append(slot)
+            self._free_slots.sort()
+
     def _emit(self, req: TTSRequest, frame: torch.Tensor) -> bool:
         """Record one frame; returns whether the request stays active."""
         req.last_frame_codebooks = frame.view(1, 1, -1)
@@ -180,6 +327,7 @@ class StreamingTTSEngine:
         return True
 
     def _finish(self, req: TTSRequest) -> None:
+        self._release_slot(req)
         req.done = True
         self.block_manager.free_blocks(req.block_table)
         req.block_table = []

@@ -10,6 +10,9 @@
   (oracle/tts.py, LIFO free list), all blocks return to the pool.
 - Failure paths: a raising frame callback only warns; running out of blocks mid-decode ends
   that request alone.
+- Graph decode (the default) gives the eager engine's frames, also with staggered requests that
+  reuse slots, change batch buckets and outgrow the captured context cap, and its captured graphs
+  survive a later growth of the attention workspace.
 """
 import json
 import os
@@ -78,10 +81,11 @@ def test_reference_streaming_tts_engine(cuda):
     assert bm.num_free_blocks == 32
 
 
-def test_frames_match_reference_engine(cuda):
+@pytest.mark.parametrize("graph", [False, True])
+def test_frames_match_reference_engine(cuda, graph):
     z, cfg, model = _golden(cuda)
     bm = _bm(cfg, cuda)
-    engine = StreamingTTSEngine(model, bm, max_batch_size=cfg["max_batch"], device=str(cuda))
+    engine = StreamingTTSEngine(model, bm, max_batch_size=cfg["max_batch"], device=str(cuda), graph_decode=graph)
     tables = {}
     emit = engine._emit
 
@@ -152,12 +156,13 @@ def test_raising_callback_only_warns(cuda, capsys):
     assert bm.allocated_block_count == 0
 
 
-def test_out_of_blocks_mid_decode_ends_that_request(cuda, capsys):
+@pytest.mark.parametrize("graph", [False, True])
+def test_out_of_blocks_mid_decode_ends_that_request(cuda, capsys, graph):
     """4 blocks of 8: two 10-frame prompts take 2 blocks each; the first to need a third block
     (sequence length 16) fails and is released, after which the other one continues."""
     z, cfg, model = _golden(cuda)
     bm = _bm(cfg, cuda, num_blocks=4)
-    engine = StreamingTTSEngine(model, bm, max_batch_size=2, device=str(cuda))
+    engine = StreamingTTSEngine(model, bm, max_batch_size=2, device=str(cuda), graph_decode=graph)
     for r in range(2):
         engine.submit(torch.from_numpy(z["prompts"][r]), max_new_frames=cfg["frames"])
     done = engine.run_until_done()
@@ -169,3 +174,65 @@ def test_out_of_blocks_mid_decode_ends_that_request(cuda, capsys):
     assert np.array_equal(torch.stack(done[1].generated_frames).cpu().numpy(), z["engine_frames1"])
     assert np.array_equal(torch.stack(done[0].generated_frames).cpu().numpy(), z["engine_frames0"][:7])
     assert bm.allocated_block_count == 0 and bm.num_free_blocks == 4
+
+
+def _run(model, cfg, cuda, requests, graph, max_batch, num_blocks, before_step=None):
+    bm = _bm(cfg, cuda, num_blocks=num_blocks)
+    engine = StreamingTTSEngine(model, bm, max_batch_size=max_batch, device=str(cuda), graph_decode=graph)
+    for prompt, frames in requests:
+        engine.submit(prompt, max_new_frames=frames)
+    steps = 0
+    while engine.active or engine.queue:
+        if before_step is not None:
+            before_step(steps)
+        engine.step()
+        steps += 1
+    out = {q.id: torch.stack(q.generated_frames).cpu().numpy() for q in engine.completed}
+    assert bm.allocated_block_count == 0
+    return out, engine
+
+
+def _staggered(cfg, n=7, seed=5):
+    g = torch.Generator().manual_seed(seed)
+    reqs = []
+    for i in range(n):
+        p = int(torch.randint(1, 40, (1,), generator=g))
+        f = int(torch.randint(1, 30, (1,), generator=g))
+        reqs.append((torch.randint(0, cfg["vocab_size"], (p, cfg["num_codebooks"]), generator=g), f))
+    reqs.append((torch.randint(0, cfg["vocab_size"], (240, cfg["num_codebooks"]), generator=g), 40))  # past 256
+    return reqs
+
+
+def test_graph_decode_matches_eager_with_slot_reuse_and_cap_growth(cuda):
+    z, cfg, model = _golden(cuda)
+    reqs = _staggered(cfg)
+    eager, _ = _run(model, cfg, cuda, reqs, False, 4, 128)
+    graph, eng = _run(model, cfg, cuda, reqs, True, 4, 128)
+    assert eng._cap >= 512  # the 240-frame prompt outgrew the first cap
+    assert sorted(graph) == sorted(eager) == list(range(len(reqs)))
+    for r in eager:
+        assert graph[r].shape == (reqs[r][1], cfg["num_codebooks"])
+        assert np.array_equal(graph[r], eager[r]), r
+
+
+def test_graphs_survive_workspace_growth(cuda):
+    """The captured graphs keep the attention workspace they were captured with alive: after an
+    eager call grows the device's workspace, replays still produce the eager frames and do not
+    write into memory handed out after the growth."""
+    from speech_serving import native
+
+    z, cfg, model = _golden(cuda)
+    reqs = [(torch.from_numpy(z["prompts"][r]), cfg["frames"]) for r in range(cfg["requests"])]
+    junk = []
+
+    def grow(step):
+        if step == 3:  # graphs for the first buckets are captured by now
+            ws = native.reserve_workspace(0, cuda)
+            native.reserve_workspace(ws.numel() * 4, cuda)
+            for _ in range(8):  # fresh allocations that could land on the old workspace
+                junk.append(torch.full((ws.numel() // 4,), 7, dtype=torch.int32, device=cuda))
+
+    graph, _ = _run(model, cfg, cuda, reqs, True, cfg["max_batch"], cfg["num_blocks"], before_step=grow)
+    for r in range(cfg["requests"]):
+        assert np.array_equal(graph[r], z[f"engine_frames{r}"]), r
+    assert junk and all(bool((t == 7).all()) for t in junk)
