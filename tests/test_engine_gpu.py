@@ -196,6 +196,34 @@ def test_graph_decode_matches_eager(cuda, dtype):
     assert results["eager"] == results["graph"]
 
 
+def test_graphs_survive_workspace_growth(cuda):
+    """After the buckets are captured, an eager call grows the device's attention workspace (which
+    drops the old buffer) and fresh allocations follow: the graphs still decode the eager tokens and
+    write nothing into memory handed out after the growth."""
+    dtype = torch.float16
+    m = random_model(cuda, 42, dtype, vocab_size=100)
+    gen = torch.Generator().manual_seed(43)
+    mels = [torch.randn(80, 200 + 30 * i, generator=gen).to(cuda, dtype) for i in range(3)]
+    prompt = torch.tensor([[1, 2]])
+    results, junk = {}, []
+    for mode in ("eager", "graph"):
+        enc, dec = pools(m, cuda, dtype)
+        kw = dict(graph_decode=True, graph_readback_k=4, graph_direct_encoder_kv=True) if mode == "graph" else {}
+        s = PhaseAwareSpeechScheduler(m, DualCacheManager(enc, dec), max_batch_size=4, device=str(cuda), **kw)
+        for mel in mels:
+            s.submit(mel, prompt_token_ids=prompt, max_new_tokens=10)
+        s.step()
+        if mode == "graph":
+            assert s.graph_buffers is not None and s.graph_buffers.graphs
+            ws = native.reserve_workspace(0, cuda)
+            native.reserve_workspace(ws.numel() * 4, cuda)
+            for _ in range(8):
+                junk.append(torch.full((ws.numel() // 4,), 7, dtype=torch.int32, device=cuda))
+        results[mode] = [r.generated_tokens for r in sorted(s.run_until_done(), key=lambda r: r.id)]
+    assert results["eager"] == results["graph"]
+    assert junk and all(bool((t == 7).all()) for t in junk)
+
+
 def test_graph_eos_is_trimmed_eager_keeps_it(cuda):
     """Graph decode drops EOS and later tokens; eager keeps EOS as the last token
     (reference test_speech_engine.py:893-933 vs :549-613)."""
