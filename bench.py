@@ -15,6 +15,8 @@ x 64, batch 64):
   large_v3_paged_attention  the same fused kernel at ctx U[1, 452] (and at batch 128,
                             the large-v3 serving configuration's slot count)
   large_v3_cross_attention  attention over 1500 contiguous encoder positions
+  large_v3_append / _gather the standalone append (encoder K/V store) and block-table
+                            gather kernels
   tts_decode                the streaming multi-codebook TTS engine (reference TTS
                             model's default shape, 64 requests x 256 frames)
   large_v3_decode           end-to-end greedy decode through the scheduler's
@@ -277,6 +279,51 @@ def large_v3_kernels(torch, native, dev, a):
         "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
         "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1), "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     del kvs, fns
+    torch.cuda.empty_cache()
+    return out
+
+
+def large_v3_append_gather(torch, native, dev, a):
+    """Standalone append and block-table gather at Whisper-large-v3 shapes (bf16, 20 heads x 64).
+
+    append: one layer's K and V rows of 64 requests x 1500 encoder positions into a paged pool through
+    a seeded permutation of its slots (the encoder K/V store); bytes = rows read + rows written + slots.
+    gather: the decoder pool of a batch of 64 (ctx U[1,452], longest-first) into zero-padded
+    [64, 20, 452, 64] K and V; bytes = pool rows read + padded output written + table entries."""
+    dt, h, d, bs = torch.bfloat16, 20, 64, 16
+    out = {}
+    n = 64 * 1500
+    g = torch.Generator(device=dev).manual_seed(a.seed + 300)
+    kn = torch.randn(n, h, d, generator=g, device=dev, dtype=dt)
+    vn = torch.randn(n, h, d, generator=g, device=dev, dtype=dt)
+    nb = n // bs
+    kp = torch.zeros(nb, bs, h, d, device=dev, dtype=dt)
+    vp = torch.zeros_like(kp)
+    slots = torch.randperm(nb, generator=torch.Generator().manual_seed(a.seed + 301))
+    slots = (slots[:, None] * bs + torch.arange(bs)[None]).reshape(-1).to(dev)
+    avg = graph_launch_us(torch, [lambda: native.append(kn, vn, kp, vp, slots)], per_fn=4, replays=5)
+    byts = n * (2 * h * d * 2 + 2 * h * d * 2 + 8)
+    out["large_v3_append"] = {
+        "shape": "bf16, 20 heads x 64, 64 requests x 1500 encoder positions (one layer's K and V) into a paged "
+                 "pool through a permuted slot mapping",
+        "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
+        "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1), "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del kn, vn, kp, vp, slots
+    torch.cuda.empty_cache()
+
+    sets = paged_sets(torch, native, dev, dt, 64, h, d, bs, 4096, 452, a.seed + 100, 0, True)
+    outs = (torch.empty(64, h, 452, d, device=dev, dtype=dt), torch.empty(64, h, 452, d, device=dev, dtype=dt))
+    fns = [lambda s=s: native.gather(s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, k_out=outs[0], v_out=outs[1])
+           for s in sets]
+    avg = graph_launch_us(torch, fns)
+    byts = sum(2 * sum(s.ctx.tolist()) * h * d * 2 + 2 * 64 * h * 452 * d * 2 +
+               4 * sum(math.ceil(c / bs) for c in s.ctx.tolist()) + 4 * 64 for s in sets) / len(sets)
+    out["large_v3_gather"] = {
+        "shape": "bf16, 20 heads x 64, batch 64, ctx U[1,452] longest-first, block size 16, into zero-padded "
+                 "[64, 20, 452, 64] K and V",
+        "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
+        "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1), "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    del sets, fns, outs
     torch.cuda.empty_cache()
     return out
 
@@ -544,6 +591,7 @@ def main():
     torch.cuda.empty_cache()
     if not a.no_large_v3:
         result.update(large_v3_kernels(torch, native, dev, a))
+        result.update(large_v3_append_gather(torch, native, dev, a))
         if not a.no_decode:
             result["large_v3_decode"] = large_v3_decode(torch, dev, a)
     if not a.no_tts:

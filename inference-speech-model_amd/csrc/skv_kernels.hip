@@ -73,6 +73,37 @@ namespace {
 // ---------------------------------------------------------------------------
 // Append: pool[slot] = new row, 16 bytes per thread, K in grid.y 0, V in 1.
 // ---------------------------------------------------------------------------
+// Division by a launch-constant divisor d without a divide: m = floor(2^32 / d)
+// (2^32 - 1 for d = 1), so umulhi(n, m) is floor(n / d) or one less for every
+// n < 2^32, and one remainder test corrects it.
+struct DivU32 {
+  uint32_t d, m;
+};
+DivU32 make_div(uint32_t d) { return {d, d == 1 ? 0xffffffffu : (uint32_t)((1ull << 32) / d)}; }
+__device__ __forceinline__ uint32_t udiv(uint32_t n, DivU32 f) {
+  uint32_t q = __umulhi(n, f.m);
+  if (n - q * f.d >= f.d) ++q;
+  return q;
+}
+
+// Append with 32-bit element indices (total rows * heads * vectors < 2^31).
+__global__ __launch_bounds__(256) void append32_kernel(const uint4* __restrict__ k_new, const uint4* __restrict__ v_new,
+                                                       int64_t sn, int64_t sh, uint4* __restrict__ k_pool,
+                                                       uint4* __restrict__ v_pool, const int64_t* __restrict__ slots,
+                                                       uint32_t total, DivU32 per_tok, DivU32 vpr, int64_t num_slots) {
+  const uint4* src = blockIdx.y == 0 ? k_new : v_new;
+  uint4* dst = blockIdx.y == 0 ? k_pool : v_pool;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    const uint32_t n = udiv(i, per_tok);
+    const uint32_t r = i - n * per_tok.d;
+    const uint32_t h = udiv(r, vpr);
+    const uint32_t c = r - h * vpr.d;
+    const int64_t slot = slots[n];
+    if (slot < 0 || slot >= num_slots) continue;
+    dst[slot * per_tok.d + r] = src[(int64_t)n * sn + (int64_t)h * sh + c];
+  }
+}
+
 __global__ __launch_bounds__(256) void append_kernel(const uint4* __restrict__ k_new, const uint4* __restrict__ v_new,
                                                      int64_t sn, int64_t sh, uint4* __restrict__ k_pool,
                                                      uint4* __restrict__ v_pool, const int64_t* __restrict__ slots,
@@ -96,6 +127,39 @@ __global__ __launch_bounds__(256) void append_kernel(const uint4* __restrict__ k
 // Gather: out[b, h, t, :] = pool[table[b][t / bs] * bs + t % bs, h, :] for
 // t < lens[b], zero otherwise. Output [B, H, T, D] contiguous.
 // ---------------------------------------------------------------------------
+// Gather with 32-bit element indices (batch * heads * T * vectors < 2^31).
+__global__ __launch_bounds__(256) void gather32_kernel(const uint4* __restrict__ k_pool, const uint4* __restrict__ v_pool,
+                                                       const int32_t* __restrict__ tables, int32_t tstride,
+                                                       const int32_t* __restrict__ lens, uint4* __restrict__ k_out,
+                                                       uint4* __restrict__ v_out, uint32_t total, DivU32 per_row,
+                                                       DivU32 per_head, DivU32 vpr, DivU32 bs, int32_t heads, int32_t nb,
+                                                       int32_t T) {
+  const uint4* src = blockIdx.y == 0 ? k_pool : v_pool;
+  uint4* dst = blockIdx.y == 0 ? k_out : v_out;
+  const int64_t lim = (int64_t)tstride * bs.d;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    const uint32_t b = udiv(i, per_row);
+    uint32_t r = i - b * per_row.d;
+    const uint32_t h = udiv(r, per_head);
+    r -= h * per_head.d;
+    const uint32_t t = udiv(r, vpr);
+    const uint32_t c = r - t * vpr.d;
+    int64_t len = lens[b];
+    len = len < T ? len : T;
+    len = len < lim ? len : lim;
+    uint4 val = make_uint4(0u, 0u, 0u, 0u);
+    if ((int64_t)t < len) {
+      const uint32_t bi = udiv(t, bs);
+      const int32_t blk = tables[(int64_t)b * tstride + bi];
+      if ((uint32_t)blk < (uint32_t)nb) {
+        const int64_t tok = (int64_t)blk * bs.d + (t - bi * bs.d);
+        val = src[(tok * heads + h) * vpr.d + c];
+      }
+    }
+    dst[i] = val;
+  }
+}
+
 __global__ __launch_bounds__(256) void gather_kernel(const uint4* __restrict__ k_pool, const uint4* __restrict__ v_pool,
                                                      const int32_t* __restrict__ tables, int32_t tstride,
                                                      const int32_t* __restrict__ lens, uint4* __restrict__ k_out,
@@ -1213,10 +1277,17 @@ int skv_append(const void* k_new, const void* v_new, int64_t new_stride_n, int64
   const int64_t total = (int64_t)n_tokens * num_heads * vpr;
   int64_t blocks = cdiv(total, 256);
   if (blocks > 65535) blocks = 65535;
-  hipLaunchKernelGGL(append_kernel, dim3((uint32_t)blocks, v_new ? 2 : 1), dim3(256), 0, (hipStream_t)stream,
-                     (const uint4*)k_new, (const uint4*)(v_new ? v_new : k_new), new_stride_n / epl,
-                     new_stride_h / epl, (uint4*)k_pool, (uint4*)(v_pool ? v_pool : k_pool), slot_mapping, n_tokens,
-                     num_heads, vpr, num_slots);
+  if (total < ((int64_t)1 << 31)) {
+    hipLaunchKernelGGL(append32_kernel, dim3((uint32_t)blocks, v_new ? 2 : 1), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4*)k_new, (const uint4*)(v_new ? v_new : k_new), new_stride_n / epl,
+                       new_stride_h / epl, (uint4*)k_pool, (uint4*)(v_pool ? v_pool : k_pool), slot_mapping,
+                       (uint32_t)total, make_div((uint32_t)(num_heads * vpr)), make_div((uint32_t)vpr), num_slots);
+  } else {
+    hipLaunchKernelGGL(append_kernel, dim3((uint32_t)blocks, v_new ? 2 : 1), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4*)k_new, (const uint4*)(v_new ? v_new : k_new), new_stride_n / epl,
+                       new_stride_h / epl, (uint4*)k_pool, (uint4*)(v_pool ? v_pool : k_pool), slot_mapping,
+                       n_tokens, num_heads, vpr, num_slots);
+  }
   return check_launch("skv_append");
 }
 
@@ -1239,10 +1310,19 @@ int skv_gather(const void* k_pool, const void* v_pool, const int32_t* block_tabl
   const int64_t total = (int64_t)batch * num_heads * max_len * vpr;
   int64_t blocks = cdiv(total, 256);
   if (blocks > 65535) blocks = 65535;
-  hipLaunchKernelGGL(gather_kernel, dim3((uint32_t)blocks, v_pool ? 2 : 1), dim3(256), 0, (hipStream_t)stream,
-                     (const uint4*)k_pool, (const uint4*)(v_pool ? v_pool : k_pool), block_tables, table_stride, lens,
-                     (uint4*)k_out, (uint4*)(v_out ? v_out : k_out), batch, num_heads, vpr, block_size, num_blocks,
-                     max_len);
+  if (total < ((int64_t)1 << 31)) {
+    const uint32_t per_head = (uint32_t)max_len * (uint32_t)vpr;
+    hipLaunchKernelGGL(gather32_kernel, dim3((uint32_t)blocks, v_pool ? 2 : 1), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4*)k_pool, (const uint4*)(v_pool ? v_pool : k_pool), block_tables, table_stride,
+                       lens, (uint4*)k_out, (uint4*)(v_out ? v_out : k_out), (uint32_t)total,
+                       make_div(per_head * (uint32_t)num_heads), make_div(per_head), make_div((uint32_t)vpr),
+                       make_div((uint32_t)block_size), num_heads, num_blocks, max_len);
+  } else {
+    hipLaunchKernelGGL(gather_kernel, dim3((uint32_t)blocks, v_pool ? 2 : 1), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4*)k_pool, (const uint4*)(v_pool ? v_pool : k_pool), block_tables, table_stride,
+                       lens, (uint4*)k_out, (uint4*)(v_out ? v_out : k_out), batch, num_heads, vpr, block_size,
+                       num_blocks, max_len);
+  }
   return check_launch("skv_gather");
 }
 
