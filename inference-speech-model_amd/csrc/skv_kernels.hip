@@ -804,9 +804,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
   auto score_new_key = [&]() {
     if (new_begin >= t_begin && new_begin < t_end && wave == kWaves - 1) {
       if constexpr (PAGED && FAST) {
-        // The LDS copy has landed once this wave's loads have all completed.
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        if (g == 0) {
+        if (g == 0) {  // the LDS copy has landed (the caller waited for it)
           nk = s_new[0][lane];
           nv = s_new[1][lane];
         }
@@ -936,7 +934,13 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
           softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
         }
         if constexpr (decltype(last_wave)::value) {
-          if (one_new) score_new_key();
+          if (one_new) {
+            // The LDS copy has landed once this wave's loads have all completed; wait
+            // for it whether or not this chunk scores the new key, so no copy is in
+            // flight when the workgroup ends.
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            score_new_key();
+          }
         }
       };
       if (__builtin_amdgcn_readfirstlane(wave) == kWaves - 1)
