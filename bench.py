@@ -369,9 +369,42 @@ def large_v3_decode(torch, dev, a):
         "wall_s_incl_prefill": round(wall, 3),
         "completed_ok": ok,
     }
-    del sched, model, dec, enc
+    del sched, dec, enc
     torch.cuda.empty_cache()
+    if not a.no_cpu_baseline:
+        res["cpu_baseline"] = decode_cpu_baseline(model, states, WHISPER_DEFAULT_PREFIX_TOKENS, 8.0)
+    del model
     return res
+
+
+def decode_cpu_baseline(model, states, prompt, budget_s):
+    """The numpy oracle of the decoder (float64, one thread) decoding one request greedily with its
+    contiguous past, as the reference's eager path does per request: decode tokens/s (the prompt's
+    prefill is not timed). Same weights and encoder states as the GPU decode."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import decoder as D
+
+    import torch
+
+    with torch.no_grad():  # the encoder K/V are inputs of the decode: projected on the GPU
+        cross = [(k.double().cpu().numpy(), v.double().cpu().numpy()) for k, v in model.project_cross_kv(states)]
+    state = {k: v.float().cpu().numpy() for k, v in model.state_dict().items()}
+    m = D.Model(state, model.num_heads, model.head_dim)
+    del state
+    with threadpool_limits(limits=1):
+        logits, past = m.decode_step(np.asarray([list(prompt)]), None, cross)
+        tokens = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget_s:
+            t = int(np.argmax(logits[0, -1]))
+            logits, past = m.decode_step(np.asarray([[t]]), past, cross)
+            tokens += 1
+        el = time.perf_counter() - t0
+    return {"value": round(tokens / el, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{tokens} greedy decode tokens of one request (context {len(prompt) + 1}.."
+                      f"{len(prompt) + tokens}, 1500 encoder positions) by the numpy oracle"}
 
 
 def tts_decode(torch, dev, a):
