@@ -8,12 +8,15 @@ written from the reference's source text (file:line cited per function):
                       attention = gather + attention.
     oracle.decoder    the synthetic Whisper-class decoder (DecoderLayer.forward,
                       decode_step, greedy decoding) used for token parity.
+    oracle.tts        the streaming multi-codebook TTS model (codebook embedding
+                      sum, decoder layers, per-codebook heads, frame-by-frame
+                      greedy generation) and the TTS engine's block bookkeeping.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import
 anything from this package, and only as the checker (or, in bench.py, as the
 timed CPU baseline). The product path (speech_serving) never imports it.
 
 Pinning: every oracle function is checked in tests/test_oracle.py against
-closed forms, invariants, brute force on tiny inputs and (for the decoder)
-golden vectors in tests/golden/. See each test for which function it pins.
+closed forms, invariants, brute force on tiny inputs and (for the decoder and
+the TTS model) golden vectors in tests/golden/. See each test for which function it pins.
 """
