@@ -16,7 +16,8 @@ Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import
 anything from this package, and only as the checker (or, in bench.py, as the
 timed CPU baseline). The product path (speech_serving) never imports it.
 
-Pinning: every oracle function is checked in tests/test_oracle.py against
-closed forms, invariants, brute force on tiny inputs and (for the decoder and
-the TTS model) golden vectors in tests/golden/. See each test for which function it pins.
+Pinning: every oracle function is checked (tests/test_oracle.py,
+tests/test_tts_oracle.py) against closed forms, invariants, brute force on tiny
+inputs and (for the decoder and the TTS model) golden vectors in tests/golden/.
+See each test for which function it pins.
 """
