@@ -23,6 +23,10 @@ x 64, batch 64):
                             captured graphs: 32 layers, d_model 1280, vocab
                             51866, N(0, 0.02) weights, 64 requests x 448 tokens,
                             random N(0,1) encoder states projected by cross_attn_k/v.
+  large_v3_serving          the large-v3 serving scenario: 128 graph slots, a burst of
+                            256 requests x 448 tokens at t=0, a decoder pool that holds
+                            the 128 slots' blocks but not the burst's, so admission waits
+                            for freed blocks and recycles them.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline] [--no-large-v3]
     python bench.py --mode copy    # known-size copy for PMC counter scaling
@@ -65,9 +69,11 @@ def parse():
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--decode-tokens", type=int, default=448)
     ap.add_argument("--decode-layers", type=int, default=32)
-    ap.add_argument("--mode", choices=["attention", "copy", "decode", "tts"], default="attention",
+    ap.add_argument("--no-serving", action="store_true", help="skip the large-v3 256-request serving burst")
+    ap.add_argument("--mode", choices=["attention", "copy", "decode", "serving", "tts"], default="attention",
                     help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling; "
-                         "decode: only the large-v3-shaped greedy decode; tts: only the streaming TTS engine")
+                         "decode: only the large-v3-shaped greedy decode; serving: only the large-v3 serving "
+                         "burst; tts: only the streaming TTS engine")
     ap.add_argument("--copy-mib", type=int, default=512)
     return ap.parse_args()
 
@@ -377,6 +383,66 @@ def large_v3_decode(torch, dev, a):
     return res
 
 
+def large_v3_serving(torch, dev, a):
+    """The large-v3 serving scenario: 128 graph slots, a burst of 256 requests x 448 greedy tokens at
+    t=0, a decoder pool of 128 x 29 + 100 blocks (the graph path reserves ceil((4 + 448) / 16) = 29
+    blocks per request up front), so the second half of the burst is admitted as blocks free up."""
+    from speech_serving import (BlockManager, DualCacheManager, EncoderBlockManager, MemoryGuard,
+                                PhaseAwareSpeechScheduler, WhisperClassSpeechEncoderDecoderModel)
+    from speech_serving.phase_aware_scheduler import WHISPER_DEFAULT_PREFIX_TOKENS
+
+    dt, L, dm, h, vocab, t_enc, bs = torch.bfloat16, a.decode_layers, 1280, 20, 51866, 1500, 16
+    slots, burst, n, distinct = 128, 256, a.decode_tokens, 16
+    model = WhisperClassSpeechEncoderDecoderModel(0, L, h, dm, 128, vocab, head_dim=64).to(dev, dt).eval()
+    model.init_normal_(0.02, seed=a.seed, draw_device=str(dev))
+    per_req = math.ceil((len(WHISPER_DEFAULT_PREFIX_TOKENS) + n) / bs)
+    pool = slots * per_req + 100
+    dec = BlockManager(L, h, 64, bs, num_blocks=pool, dtype=dt, device=str(dev))
+    enc = EncoderBlockManager(1, h, 64, bs, num_blocks=8, dtype=dt, device=str(dev))
+    # Admission backpressure off: every request queues and waits for a slot and for blocks.
+    sched = PhaseAwareSpeechScheduler(model, DualCacheManager(enc, dec), MemoryGuard(high_water_mark_pct=1e9),
+                                      max_batch_size=slots, device=str(dev), eos_token_id=-1, graph_decode=True,
+                                      graph_readback_k=4, graph_direct_encoder_kv=True, graph_max_enc_len=t_enc)
+    g = torch.Generator(device=dev).manual_seed(a.seed + 11)
+    with torch.no_grad():
+        # The burst shares 16 distinct encoder outputs (each request still gets its own slot copy).
+        kvs = [model.project_cross_kv(torch.randn(1, t_enc, dm, generator=g, device=dev, dtype=dt))
+               for _ in range(distinct)]
+        for i in range(burst):
+            sched.submit_encoded(kvs[i % distinct], prompt_token_ids=torch.tensor([WHISPER_DEFAULT_PREFIX_TOKENS]),
+                                 max_new_tokens=n)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    peak = 0
+    while sched.step():
+        peak = max(peak, dec.allocated_block_count)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    done = sched.completed
+    generated = sum(len(r.generated_tokens) for r in done)
+    decode_tokens = sum(len(r.generated_tokens) - 1 for r in done)
+    ok = (len(done) == burst and all(len(r.generated_tokens) == n for r in done) and peak <= pool
+          and dec.allocated_block_count == 0 and any(r.graph_slot_reused for r in done))
+    res = {
+        "workload": f"Whisper-large-v3-shaped serving burst: {L} layers, d_model {dm}, {h} heads x 64, vocab {vocab}, "
+                    f"bf16 N(0,0.02) weights, {slots} graph slots (buckets 1/8/16/32/64/128), {burst} requests x "
+                    f"{n} tokens submitted at t=0 (4-token prompt, {t_enc} encoder positions, {distinct} distinct "
+                    f"N(0,1) encoder outputs), decoder pool {pool} blocks of {bs} (< {burst} x {per_req}), "
+                    f"readback every 4 steps",
+        "decode_tokens_per_s": round(decode_tokens / sched.decode_time_s, 1),
+        "ms_per_decode_step": round(sched.decode_time_s / max(sched.decode_steps, 1) * 1e3, 3),
+        "decode_steps": sched.decode_steps,
+        "tokens_per_s_incl_admission": round(generated / wall, 1),
+        "wall_s": round(wall, 3),
+        "peak_blocks": peak,
+        "pool_blocks": pool,
+        "completed_ok": ok,
+    }
+    del sched, dec, enc, kvs, model
+    torch.cuda.empty_cache()
+    return res
+
+
 def decode_cpu_baseline(model, states, prompt, budget_s):
     """The numpy oracle of the decoder (float64, one thread) decoding one request greedily with its
     contiguous past, as the reference's eager path does per request: decode tokens/s (the prompt's
@@ -507,6 +573,10 @@ def main():
         native.lib()
         print(json.dumps({"large_v3_decode": large_v3_decode(torch, dev, a)}))
         return
+    if a.mode == "serving":  # the large-v3 serving burst alone
+        native.lib()
+        print(json.dumps({"large_v3_serving": large_v3_serving(torch, dev, a)}))
+        return
     if a.mode == "tts":  # the streaming TTS engine alone
         native.lib()
         print(json.dumps({"tts_decode": tts_decode(torch, dev, a)}))
@@ -631,6 +701,8 @@ def main():
         result.update(large_v3_append_gather(torch, native, dev, a))
         if not a.no_decode:
             result["large_v3_decode"] = large_v3_decode(torch, dev, a)
+        if not a.no_serving:
+            result["large_v3_serving"] = large_v3_serving(torch, dev, a)
     print(json.dumps(result), flush=True)
 
 

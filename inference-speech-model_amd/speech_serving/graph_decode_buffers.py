@@ -225,6 +225,14 @@ class GraphDecodeBuffers:
         self.g_slot_finished[slot_idx].zero_()
         return slot_idx
 
+    def set_first_token(self, slot_idx: int, tok: int) -> None:
+        """Record the first token of a slot bound before its prefill ran (the scheduler binds the
+        slots of a step's admissions, prefills them as one batch, then sets each first token)."""
+        s = self.slots[slot_idx]
+        s.last_token_id = tok
+        s.pending_tokens = [tok]
+        self.g_slot_tokens[slot_idx].fill_(int(tok))
+
     def release_slot(self, slot_idx: int) -> None:
         s = self.slots[slot_idx]
         s.active = False

@@ -347,6 +347,7 @@ class PhaseAwareSpeechScheduler:
 
     def _process_encode_phase(self) -> None:
         enc_bm = self.dual_cache.encoder_bm
+        placed = len(self.active_encode)
         while self._admission_slots() > 0 and self.queue:
             req = self.queue[0]
             mel_in = req.mel_features.unsqueeze(0) if req.mel_features.dim() == 2 else req.mel_features
@@ -398,13 +399,18 @@ class PhaseAwareSpeechScheduler:
                                                      enc_time=time.perf_counter() - t0)
             except Exception as e:  # deterministic cleanup, reference :558-560
                 logger.error(f"Error in ENCODE_PHASE for req {req.id}: {e}", exc_info=True)
+                if req in self.active_encode:
+                    self.active_encode.remove(req)
                 self._complete_request(req, status=RequestPhase.FAILED)
+        if len(self.active_encode) > placed:
+            self._prefill_admitted(self.active_encode[placed:])
 
     def _setup_request_after_encode(self, req: DualCacheRequest, encoder_hidden: Optional[torch.Tensor],
                                     encoder_kv_list: List[Tuple[torch.Tensor, torch.Tensor]],
                                     full_hash: Optional[str] = None, enc_time: float = 0.0,
                                     enc_seq_len: Optional[int] = None, use_encoder_pool: bool = True) -> None:
-        """Place the encoder K/V, prefill the prompt into the paged pool, emit the first token."""
+        """Place the encoder K/V, allocate the decoder blocks and (graph decode) bind a slot. The prompt
+        prefill and the first token follow in _prefill_admitted, batched over the step's admissions."""
         enc_bm, dec_bm = self.dual_cache.encoder_bm, self.dual_cache.decoder_bm
         t_enc = enc_seq_len if enc_seq_len is not None else encoder_hidden.shape[1]
         req.encoder_seq_len = t_enc
@@ -435,16 +441,20 @@ class PhaseAwareSpeechScheduler:
         req.encode_done_time = time.perf_counter()
         req.phase = RequestPhase.DECODE_PHASE
 
-        prompt = req.prompt_token_ids.to(self.device).view(1, -1)
-        p = prompt.shape[1]
+        p = req.prompt_token_ids.shape[-1]
         req.decoder_seq_len = p
         total = p + req.max_new_tokens if self.graph_decode else p
         for _ in range(-(-total // dec_bm.block_size)):
             req.decoder_block_table.append(self.dual_cache.allocate_decoder_block())
 
-        # Cross-attention K/V for prefill (and for eager decode: the arena slot).
+        # Cross-attention K/V for the prefill and the decode: the request's graph slot (filled by
+        # assign_slot) or its arena slot (eager decode).
         if self.graph_decode:
-            cross = self._direct_cross(encoder_kv_list, t_enc)
+            slot = self.graph_buffers.assign_slot(req=req, enc_kv_layers=encoder_kv_list, prompt_len=p,
+                                                  initial_tok=0, initial_self_kv=None)
+            req.slot_idx = slot
+            req.graph_slot_idx = slot
+            req.graph_slot_reused = self.graph_buffers.slots[slot].reused
         else:
             if req.encoder_block_table:
                 s, _ = self.cross_arena.put_from_pool(enc_bm, req.encoder_block_table, t_enc,
@@ -452,29 +462,80 @@ class PhaseAwareSpeechScheduler:
             else:
                 s, _ = self.cross_arena.put(encoder_kv_list)
             req.cross_slot = s
-            cross = self._arena_cross([s], [t_enc], req.cross_layers)
-        tables = torch.tensor([req.decoder_block_table], dtype=torch.int32, device=self.device)
-        ctx = torch.tensor([p], dtype=torch.int32, device=self.device)
-        kv = PagedKV(dec_bm.key_pool, dec_bm.value_pool, tables, ctx, p)
+        self.active_encode.append(req)
+
+    def _prefill_admitted(self, reqs: List[DualCacheRequest]) -> None:
+        """Prefill the prompts of the requests placed in this step and emit their first tokens.
+
+        The reference prefills each request alone and reads its first token back with .item()
+        (phase_aware_scheduler.py:664-703). Here the requests that share a prompt length and a
+        cross-attention layer count run as one batch: one decode_step_paged over B x P prompt tokens
+        (fused causal append into each request's blocks) and one token readback per batch. A batch
+        that fails fails its requests, like a failed decode step. First tokens are then emitted in
+        admission order."""
+        groups: Dict[Tuple[int, int, bool], List[DualCacheRequest]] = {}
+        for r in reqs:
+            # A graph slot holds at most max_enc_len encoder positions; a longer encoder output
+            # prefills from its own tensors (one request per launch).
+            direct = self.graph_decode and r.encoder_seq_len > self.graph_buffers.max_enc_len
+            groups.setdefault((r.prompt_token_ids.shape[-1], r.cross_layers, direct), []).append(r)
+        first: Dict[int, int] = {}
+        for (p, layers, direct), rs in groups.items():
+            for part in ([[r] for r in rs] if direct else [rs]):
+                try:
+                    toks = self._prefill(part, p, layers, direct)
+                except Exception as e:
+                    logger.error(f"Error in prefill of reqs {[r.id for r in part]}: {e}", exc_info=True)
+                    for r in part:
+                        self.active_encode.remove(r)
+                        self._complete_request(r, status=RequestPhase.FAILED)
+                    continue
+                first.update((id(r), t) for r, t in zip(part, toks))
+        now = time.perf_counter()
+        for req in reqs:
+            if id(req) not in first:
+                continue
+            tok = first[id(req)]
+            self.active_encode.remove(req)
+            req.last_token_id = tok
+            req.generated_tokens.append(tok)
+            req.generated_count += 1
+            req.first_token_time = now
+            if (req.eos_token_id is not None and tok == req.eos_token_id) or req.generated_count >= req.max_new_tokens:
+                self._complete_request(req, status=RequestPhase.COMPLETED)
+                continue
+            self.active_decode.append(req)
+            if self.graph_decode:
+                self.graph_buffers.set_first_token(req.slot_idx, tok)
+            if self.avoid_redundant_cross_kv:
+                req.cached_encoder_kv = None
+
+    def _prefill(self, reqs: List[DualCacheRequest], p: int, layers: int, direct: bool) -> List[int]:
+        """One batched prefill of len(reqs) prompts of p tokens; returns each request's first token."""
+        dec_bm = self.dual_cache.decoder_bm
+        n = len(reqs)
+        prompts = torch.cat([r.prompt_token_ids.reshape(1, p) for r in reqs]).to(self.device)
+        width = max(len(r.decoder_block_table) for r in reqs)
+        meta = torch.full((n * width + n,), -1, dtype=torch.int32)  # tables [n, width], then lengths [n]
+        for i, r in enumerate(reqs):
+            meta[i * width: i * width + len(r.decoder_block_table)] = torch.tensor(r.decoder_block_table,
+                                                                                   dtype=torch.int32)
+        meta[n * width:] = p
+        meta = meta.to(self.device)
+        kv = PagedKV(dec_bm.key_pool, dec_bm.value_pool, meta[: n * width].view(n, width), meta[n * width:], p)
+        if direct:
+            cross = self._direct_cross(reqs[0].cached_encoder_kv, reqs[0].encoder_seq_len)
+        elif self.graph_decode:
+            gb = self.graph_buffers
+            ids = torch.tensor([[r.slot_idx for r in reqs], [min(r.encoder_seq_len, gb.max_enc_len) for r in reqs]],
+                               dtype=torch.int32).to(self.device)
+            cross = CrossKV([gb.g_cross_kv[:, l, 0] for l in range(layers)],
+                            [gb.g_cross_kv[:, l, 1] for l in range(layers)], ids[1], gb.max_enc_len, slot_ids=ids[0])
+        else:
+            cross = self._arena_cross([r.cross_slot for r in reqs], [r.encoder_seq_len for r in reqs], layers)
         with torch.no_grad():
-            logits = self.model.decode_step_paged(prompt, kv, cross)
-            tok = int(native.argmax(logits).item())
-        req.last_token_id = tok
-        req.generated_tokens.append(tok)
-        req.generated_count += 1
-        req.first_token_time = time.perf_counter()
-        if (req.eos_token_id is not None and tok == req.eos_token_id) or req.generated_count >= req.max_new_tokens:
-            self._complete_request(req, status=RequestPhase.COMPLETED)
-            return
-        self.active_decode.append(req)
-        if self.graph_decode:
-            slot = self.graph_buffers.assign_slot(req=req, enc_kv_layers=encoder_kv_list, prompt_len=p,
-                                                  initial_tok=tok, initial_self_kv=None)
-            req.slot_idx = slot
-            req.graph_slot_idx = slot
-            req.graph_slot_reused = self.graph_buffers.slots[slot].reused
-        if self.avoid_redundant_cross_kv:
-            req.cached_encoder_kv = None
+            logits = self.model.decode_step_paged(prompts, kv, cross)
+            return native.argmax(logits).tolist()
 
     def _direct_cross(self, enc_kv: List[Tuple[torch.Tensor, torch.Tensor]], t_enc: int) -> CrossKV:
         ks = [k for k, _ in enc_kv]
