@@ -178,6 +178,32 @@ def test_variable_length_batch_matches_sequential_oracle(cuda):
     assert enc.allocated_block_count == 0 and dec.allocated_block_count == 0
 
 
+@pytest.mark.parametrize("mode", ["eager", "graph"])
+def test_batched_prefill_mixed_prompts_matches_oracle(cuda, mode):
+    """Requests admitted in one step prefill as one batch per prompt length (here three groups, interleaved
+    in submission order); each request's tokens equal its own one-at-a-time oracle decode."""
+    m = random_model(cuda, 4242)
+    gen = torch.Generator().manual_seed(4242)
+    prompts = [[1, 2, 3], [5], [7, 8, 3, 2], [9, 4, 1], [6], [2, 2, 3, 3]]
+    mels = [torch.randn(80, 60 + 24 * i, generator=gen) for i in range(len(prompts))]
+    om = oracle_of(m)
+    want = []
+    for mel, pr in zip(mels, prompts):
+        _, kv = om.encode(mel[None].numpy())
+        want.append(om.greedy(pr, kv, 12)[0])
+    enc, dec = pools(m, cuda, bs=8)
+    kw = dict(graph_decode=True, graph_readback_k=4, graph_direct_encoder_kv=True) if mode == "graph" else {}
+    s = PhaseAwareSpeechScheduler(m, DualCacheManager(enc, dec), MemoryGuard(), max_batch_size=8,
+                                  device=str(cuda), **kw)
+    for mel, pr in zip(mels, prompts):
+        s.submit(mel.to(cuda), prompt_token_ids=torch.tensor([pr]), max_new_tokens=12)
+    s.step()  # one step admits and prefills all six
+    assert len(s.active_decode) == len(prompts) and not s.active_encode and not s.queue
+    got = [r.generated_tokens for r in sorted(s.run_until_done(), key=lambda r: r.id)]
+    assert got == want
+    assert enc.allocated_block_count == 0 and dec.allocated_block_count == 0
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_graph_decode_matches_eager(cuda, dtype):
     m = random_model(cuda, 42, dtype, vocab_size=100)
@@ -315,7 +341,7 @@ def test_failed_decode_step_releases_everything(cuda):
 
     def flaky(*a, **k):
         calls[0] += 1
-        if calls[0] == 4:  # 2 prefills, 1 decode step, then fail
+        if calls[0] == 4:  # one batched prefill of both requests, 2 decode steps, then fail
             raise RuntimeError("injected failure")
         return real(*a, **k)
 
@@ -326,6 +352,40 @@ def test_failed_decode_step_releases_everything(cuda):
     assert len(done) == 2 and all(r.phase == RequestPhase.FAILED for r in done)
     assert dec.allocated_block_count == 0 and enc.allocated_block_count == 0
     assert s.cross_arena.live == {}
+
+
+@pytest.mark.parametrize("mode", ["eager", "graph"])
+def test_failed_batched_prefill_fails_its_requests_and_releases_everything(cuda, mode):
+    """A prefill batch that raises fails the requests of that batch (blocks, arena and graph slots all
+    returned); a request admitted afterwards decodes normally."""
+    m = random_model(cuda, 8)
+    enc, dec = pools(m, cuda)
+    kw = dict(graph_decode=True, graph_readback_k=4, graph_direct_encoder_kv=True) if mode == "graph" else {}
+    s = PhaseAwareSpeechScheduler(m, DualCacheManager(enc, dec), max_batch_size=4, device=str(cuda), **kw)
+    real = m.decode_step_paged
+    calls = [0]
+
+    def flaky(*a, **k):
+        calls[0] += 1
+        if calls[0] == 1:
+            raise RuntimeError("injected prefill failure")
+        return real(*a, **k)
+
+    m.decode_step_paged = flaky
+    for _ in range(3):
+        s.submit(torch.randn(80, 64).to(cuda), max_new_tokens=6)
+    s.step()
+    assert len(s.completed) == 3 and all(r.phase == RequestPhase.FAILED for r in s.completed)
+    assert not s.active_encode and not s.active_decode
+    assert dec.allocated_block_count == 0 and enc.allocated_block_count == 0
+    if mode == "graph":
+        assert s.graph_buffers.active_slot_count() == 0
+    else:
+        assert s.cross_arena.live == {}
+    s.submit(torch.randn(80, 64).to(cuda), max_new_tokens=6)
+    done = s.run_until_done()
+    assert done[-1].phase == RequestPhase.COMPLETED and len(done[-1].generated_tokens) == 6
+    assert dec.allocated_block_count == 0 and enc.allocated_block_count == 0
 
 
 def test_config1_tiny_greedy_tokens_match_oracle(cuda):
