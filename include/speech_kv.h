@@ -34,6 +34,8 @@
  *                         cross-attention buffer. Replaces the per-layer copy_ loop
  *                         of GraphDecodeBuffers.assign_slot at
  *                         speech_serving/graph_decode_buffers.py:317-327.
+ *   skv_codebook_embed_sum  the summed per-codebook embedding rows of a multi-codebook
+ *                         frame (speech_serving/models.py:39-52) in one launch.
  *   skv_argmax            greedy sampling (first maximum) with optional on-device
  *                         token feedback per decode slot. Replaces argmax +
  *                         copy_ at speech_serving/models.py:486-487 and
@@ -250,6 +252,23 @@ SKV_API int skv_add_layernorm(const void* x, int64_t ldx, const void* y, int64_t
                               const void* gamma, const void* beta, float eps,
                               void* sum, int64_t lds, void* norm, int64_t ldn,
                               int32_t rows, int32_t hidden, int32_t dtype, void* stream);
+
+/*
+ * skv_codebook_embed_sum — the frame input of a multi-codebook model.
+ *   out[r*out_stride + d] = T_0[c_r0][d] + T_1[c_r1][d] + ... + T_{K-1}[c_r(K-1)][d],
+ *   added left to right with each partial sum rounded to dtype, so the result has
+ *   the bits of the sequential `embeds = embeds + emb_k(codes[..., k])` in that dtype.
+ *   c_rk = codes[r*codes_stride + k] (int64); a code outside [0, vocab) adds a zero row.
+ *   tables : HOST array of num_codebooks (1..16) device pointers, each [vocab, dim]
+ *            contiguous and 16-byte aligned
+ *   out    : [rows, dim] at row stride out_stride (elements); dim a multiple of the
+ *            16-byte vector.
+ * Replaces MultiCodebookEmbedding.forward, speech_serving/models.py:39-52 (one
+ * gather per codebook and K-1 adds) with one launch.
+ */
+SKV_API int skv_codebook_embed_sum(const int64_t* codes, int64_t codes_stride, int32_t rows,
+                                   const void* const* tables, int32_t num_codebooks, int32_t vocab,
+                                   int32_t dim, void* out, int64_t out_stride, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -480,6 +480,52 @@ void launch_add_layernorm(const AddNormParams& p, int vpl, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// Multi-codebook embedding sum: out[r] = T_0[c_r0] + T_1[c_r1] + ... with every
+// partial sum rounded to the tensor dtype, i.e. the bits of a sequential
+// x = x + emb_k(codes[..., k]) in that dtype. One thread per 16-byte vector.
+// ---------------------------------------------------------------------------
+constexpr int kMaxCodebooks = 16;
+
+struct EmbedSumParams {
+  const int64_t* codes;
+  int64_t codes_stride;  // elements between rows of codes
+  const uint4* tables[kMaxCodebooks];
+  uint4* out;
+  int64_t out_stride;    // 16-byte vectors between output rows
+  int64_t total;         // rows * vecs
+  int32_t books, vocab, vecs;
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void embed_sum_kernel(EmbedSumParams p) {
+  constexpr int EPL = Elt<DT>::EPL;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= p.total) return;
+  const int64_t r = idx / p.vecs;
+  const int v = (int)(idx - r * p.vecs);
+  uint4 raw[kMaxCodebooks];
+#pragma unroll
+  for (int k = 0; k < kMaxCodebooks; ++k) {  // every row load issues before the first add
+    if (k < p.books) {
+      const int64_t c = p.codes[r * p.codes_stride + k];
+      raw[k] = (c >= 0 && c < p.vocab) ? p.tables[k][c * p.vecs + v] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  float acc[EPL], e[EPL];
+  unpack16<DT>(raw[0], acc);
+#pragma unroll
+  for (int k = 1; k < kMaxCodebooks; ++k) {
+    if (k < p.books) {
+      unpack16<DT>(raw[k], e);
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) acc[i] += e[i];
+      unpack16<DT>(pack16<DT>(acc), acc);  // round the partial sum to the dtype
+    }
+  }
+  p.out[r * p.out_stride + v] = pack16<DT>(acc);
+}
+
+// ---------------------------------------------------------------------------
 // Attention.
 // ---------------------------------------------------------------------------
 #ifndef SKV_ATTN_WAVES
@@ -1447,6 +1493,47 @@ int skv_add_layernorm(const void* x, int64_t ldx, const void* y, int64_t ldy, co
     default: launch_add_layernorm<SKV_BF16>(p, vpl, s); break;
   }
   return check_launch("skv_add_layernorm");
+}
+
+int skv_codebook_embed_sum(const int64_t* codes, int64_t codes_stride, int32_t rows, const void* const* tables,
+                           int32_t num_codebooks, int32_t vocab, int32_t dim, void* out, int64_t out_stride,
+                           int32_t dtype, void* stream) {
+  const int eb = elt_bytes(dtype);
+  if (eb == 0) return fail(SKV_EDTYPE, "skv_codebook_embed_sum: unknown dtype %d", dtype);
+  const int epl = 16 / eb;
+  if (rows < 0 || num_codebooks < 1 || num_codebooks > kMaxCodebooks || vocab <= 0 || dim <= 0 || dim % epl)
+    return fail(SKV_EINVAL, "skv_codebook_embed_sum: bad sizes rows=%d codebooks=%d (1..%d) vocab=%d dim=%d "
+                "(a multiple of %d)", rows, num_codebooks, kMaxCodebooks, vocab, dim, epl);
+  if (rows == 0) return SKV_OK;
+  if (!codes || !tables || !out) return fail(SKV_EINVAL, "skv_codebook_embed_sum: null pointer argument");
+  if (codes_stride < num_codebooks || out_stride < dim || out_stride % epl || !aligned16(out))
+    return fail(SKV_EALIGN, "skv_codebook_embed_sum: bad strides (codes %lld, out %lld) or unaligned output",
+                (long long)codes_stride, (long long)out_stride);
+  EmbedSumParams p{};
+  for (int k = 0; k < num_codebooks; ++k) {
+    if (!tables[k] || !aligned16(tables[k]))
+      return fail(SKV_EALIGN, "skv_codebook_embed_sum: table %d is null or not 16-byte aligned", k);
+    p.tables[k] = (const uint4*)tables[k];
+  }
+  p.codes = codes;
+  p.codes_stride = codes_stride;
+  p.out = (uint4*)out;
+  p.out_stride = out_stride / epl;
+  p.books = num_codebooks;
+  p.vocab = vocab;
+  p.vecs = dim / epl;
+  p.total = (int64_t)rows * p.vecs;
+  if (p.total >= ((int64_t)1 << 32) - 256)  // work-items of one launch stay below 2^32
+    return fail(SKV_EINVAL, "skv_codebook_embed_sum: %d rows of %d vectors are too many", rows, p.vecs);
+  const int64_t blocks = cdiv(p.total, 256);
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((uint32_t)blocks);
+  switch (dtype) {
+    case SKV_F32: hipLaunchKernelGGL(embed_sum_kernel<SKV_F32>, grid, dim3(256), 0, s, p); break;
+    case SKV_F16: hipLaunchKernelGGL(embed_sum_kernel<SKV_F16>, grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL(embed_sum_kernel<SKV_BF16>, grid, dim3(256), 0, s, p); break;
+  }
+  return check_launch("skv_codebook_embed_sum");
 }
 
 int64_t skv_attention_workspace_bytes(int32_t rows, int32_t num_heads, int32_t head_dim, int32_t max_len,

@@ -473,13 +473,11 @@ class MultiCodebookEmbedding(nn.Module):
         self.embeddings = nn.ModuleList([nn.Embedding(vocab_size, embed_dim) for _ in range(num_codebooks)])
 
     def forward(self, input_codebooks: torch.Tensor) -> torch.Tensor:
-        """[B, S, K] codes -> [B, S, embed_dim]."""
+        """[B, S, K] codes -> [B, S, embed_dim]: the K gathers and K - 1 adds of the reference in one
+        launch, with the reference's left-to-right rounding."""
         if input_codebooks.shape[-1] != self.num_codebooks:
             raise ValueError(f"Expected {self.num_codebooks} codebooks, got {input_codebooks.shape[-1]}")
-        x = self.embeddings[0](input_codebooks[..., 0])
-        for k in range(1, self.num_codebooks):
-            x = x + self.embeddings[k](input_codebooks[..., k])
-        return x
+        return native.codebook_embed_sum(input_codebooks, [e.weight for e in self.embeddings])
 
 
 class MultiCodebookHeads(nn.Module):

@@ -48,7 +48,10 @@ SIGNATURES = {
                                      _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p]),
     "skv_add_layernorm": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_f, _c_p, _c_i64, _c_p, _c_i64,
                                    _c_i32, _c_i32, _c_i32, _c_p]),
+    "skv_codebook_embed_sum": (_c_int, [_c_p, _c_i64, _c_i32, _c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32,
+                                        _c_p]),
 }
+MAX_CODEBOOKS = 16  # kMaxCodebooks of the library
 
 
 def library_path() -> str:
@@ -533,3 +536,33 @@ def add_layernorm(x: torch.Tensor, y: Optional[torch.Tensor], weight: torch.Tens
                                  _code(x.dtype), _stream(x.device))
     _check(rc, "skv_add_layernorm")
     return (sum_out if y is not None else x), norm
+
+
+def codebook_embed_sum(codes: torch.Tensor, tables: Sequence[torch.Tensor]) -> torch.Tensor:
+    """sum_k tables[k][codes[..., k]] added left to right, each partial sum rounded to the tables'
+    dtype: the bits of the reference's `embeds = embeds + emb_k(codes[..., k])` loop
+    (speech_serving/models.py:39-52), in one launch. codes [..., K] int64; tables K x [vocab, dim].
+    A code outside [0, vocab) adds a zero row (nn.Embedding would raise)."""
+    _gpu(codes, "codes")
+    k = codes.shape[-1]
+    if not 1 <= k <= MAX_CODEBOOKS or len(tables) != k:
+        raise RuntimeError(f"codebook_embed_sum: {len(tables)} tables for {k} codebooks (1..{MAX_CODEBOOKS})")
+    vocab, dim = tables[0].shape
+    dt = tables[0].dtype
+    for i, t in enumerate(tables):
+        _gpu(t, f"tables[{i}]")
+        if t.shape != (vocab, dim) or t.dtype != dt or not t.is_contiguous() or t.data_ptr() % 16:
+            raise RuntimeError("codebook_embed_sum: tables must be contiguous [vocab, dim] of one dtype, "
+                               "16-byte aligned")
+    if dt not in _DTYPE_CODE:
+        raise RuntimeError(f"codebook_embed_sum: unsupported dtype {dt}")
+    c2 = codes.reshape(-1, k)
+    if c2.dtype != torch.int64 or c2.stride(-1) != 1:
+        c2 = c2.to(torch.int64).contiguous()
+    rows = c2.shape[0]
+    out = torch.empty(codes.shape[:-1] + (dim,), dtype=dt, device=codes.device)
+    ptrs = (ctypes.c_void_p * k)(*[t.data_ptr() for t in tables])
+    rc = lib().skv_codebook_embed_sum(c2.data_ptr(), c2.stride(0) if rows > 1 else k, rows, ptrs, k, vocab, dim,
+                                      out.data_ptr(), dim, _code(dt), _stream(codes.device))
+    _check(rc, "skv_codebook_embed_sum")
+    return out

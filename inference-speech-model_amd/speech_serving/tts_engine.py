@@ -32,7 +32,7 @@ from __future__ import annotations
 
 import time
 from dataclasses import dataclass, field
-from typing import Callable, Dict, List, Optional
+from typing import Callable, Dict, List, Optional, Tuple
 
 import torch
 
@@ -114,8 +114,8 @@ class StreamingTTSEngine:
         if batch:
             try:
                 if self.graph_decode:
-                    by_id = self._decode_graph(batch)
-                    frames = [by_id[r.id] for r in batch]
+                    rows = self._decode_graph(batch)
+                    frames = [rows[self._slot_of[r.id]] for r in batch]
                 else:
                     frames = self._decode(batch)
             except Exception as e:
@@ -264,8 +264,9 @@ class StreamingTTSEngine:
             self._graph_workspaces.append(ws)
         return g
 
-    def _decode_graph(self, batch: List[TTSRequest]) -> Dict[int, torch.Tensor]:
-        """One frame for every request of the batch via the captured step; request id -> [K] frame."""
+    def _decode_graph(self, batch: List[TTSRequest]) -> Tuple[torch.Tensor, ...]:
+        """One frame for every request of the batch via the captured step; the [K] frame of slot i is
+        element i of the returned tuple (views of one token tensor, made in one call)."""
         need = max(r.seq_len + 1 for r in batch)
         if need > self._cap:
             cap = max(256, self._cap)
@@ -294,8 +295,7 @@ class StreamingTTSEngine:
         ev.record()
         self._bank_events[i] = ev
         self._graph_for(b).replay()
-        step = self.g_tokens[:b * self.model.num_codebooks].view(b, -1).clone()
-        return {r.id: step[self._slot_of[r.id]] for r in batch}
+        return self.g_tokens[:b * self.model.num_codebooks].view(b, -1).clone().unbind(0)
 
     def _take_slot(self, req: TTSRequest, frame: torch.Tensor) -> None:
         slot = self._free_slots.pop(0)
