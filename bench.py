@@ -593,27 +593,34 @@ def main():
         native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, a.max_ctx, scale, out=s.out,
                                chunk_tokens=a.chunk, k_new=s.k_new, v_new=s.v_new)
 
-    # One captured graph per set; a step replays the next set's graph.
+    # Steps run as captured graphs of back-to-back launches, as the decode runs them: graphs[n]
+    # holds the steps of sets 0..n-1 in order, so K steps are K // nsets replays of the full
+    # rotation plus one replay of the first K mod nsets sets.
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         for s in sets:
             step(s)
     torch.cuda.current_stream().wait_stream(stream)
-    graphs = []
-    for s in sets:
+    graphs = {}
+    for n in sorted({nsets, a.steps % nsets, a.warmup % nsets} - {0}):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            step(s)
-        graphs.append(g)
+            for s in sets[:n]:
+                step(s)
+        graphs[n] = g
     torch.cuda.synchronize()
 
-    for i in range(a.warmup):
-        graphs[i % nsets].replay()
+    def run_steps(k):
+        for _ in range(k // nsets):
+            graphs[nsets].replay()
+        if k % nsets:
+            graphs[k % nsets].replay()
+
+    run_steps(a.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(a.steps):
-        graphs[i % nsets].replay()
+    run_steps(a.steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / a.steps * 1e3
@@ -661,6 +668,7 @@ def main():
             "pool_blocks": a.pool_blocks,
             "max_ctx": a.max_ctx,
             "rotating_sets": nsets,
+            "step_launch": f"captured graphs of {nsets} back-to-back steps (one per set), as the decode replays them",
             "rows": "longest-first (the engine's decode batch layout)",
             "chunk_tokens": a.chunk or native.default_chunk_tokens(a.batch, a.heads, a.head_dim, a.max_ctx, dtype),
         },
