@@ -128,6 +128,12 @@ __global__ __launch_bounds__(256) void append_kernel(const uint4* __restrict__ k
 // t < lens[b], zero otherwise. Output [B, H, T, D] contiguous.
 // ---------------------------------------------------------------------------
 // Gather with 32-bit element indices (batch * heads * T * vectors < 2^31).
+// Gather with 32-bit element indices (total output vectors < 2^31). One thread
+// copies one 16-byte column c of kGatherRows consecutive token rows of one
+// (row, head): one length read, then the rows' table reads and their pool
+// loads, all independent of each other, so each thread has kGatherRows loads
+// in flight. Output rows past the length (up to T) are written as zeros.
+constexpr int kGatherRows = 4;
 __global__ __launch_bounds__(256) void gather32_kernel(const uint4* __restrict__ k_pool, const uint4* __restrict__ v_pool,
                                                        const int32_t* __restrict__ tables, int32_t tstride,
                                                        const int32_t* __restrict__ lens, uint4* __restrict__ k_out,
@@ -138,25 +144,35 @@ __global__ __launch_bounds__(256) void gather32_kernel(const uint4* __restrict__
   uint4* dst = blockIdx.y == 0 ? k_out : v_out;
   const int64_t lim = (int64_t)tstride * bs.d;
   for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    // i enumerates (b, h, row group, c) with per_head = ceil(T / kGatherRows) * vpr.
     const uint32_t b = udiv(i, per_row);
     uint32_t r = i - b * per_row.d;
     const uint32_t h = udiv(r, per_head);
     r -= h * per_head.d;
-    const uint32_t t = udiv(r, vpr);
-    const uint32_t c = r - t * vpr.d;
+    const uint32_t tg = udiv(r, vpr);
+    const uint32_t c = r - tg * vpr.d;
+    const uint32_t t0 = tg * kGatherRows;
     int64_t len = lens[b];
     len = len < T ? len : T;
     len = len < lim ? len : lim;
-    uint4 val = make_uint4(0u, 0u, 0u, 0u);
-    if ((int64_t)t < len) {
-      const uint32_t bi = udiv(t, bs);
-      const int32_t blk = tables[(int64_t)b * tstride + bi];
-      if ((uint32_t)blk < (uint32_t)nb) {
-        const int64_t tok = (int64_t)blk * bs.d + (t - bi * bs.d);
-        val = src[(tok * heads + h) * vpr.d + c];
+    uint4 val[kGatherRows];
+#pragma unroll
+    for (int u = 0; u < kGatherRows; ++u) {
+      const uint32_t t = t0 + u;
+      val[u] = make_uint4(0u, 0u, 0u, 0u);
+      if ((int64_t)t < len) {
+        const uint32_t bi = udiv(t, bs);
+        const int32_t blk = tables[(int64_t)b * tstride + bi];
+        if ((uint32_t)blk < (uint32_t)nb) {
+          const int64_t tok = (int64_t)blk * bs.d + (t - bi * bs.d);
+          val[u] = src[(tok * heads + h) * vpr.d + c];
+        }
       }
     }
-    dst[i] = val;
+    const uint32_t o = ((b * (uint32_t)heads + h) * (uint32_t)T + t0) * vpr.d + c;
+#pragma unroll
+    for (int u = 0; u < kGatherRows; ++u)
+      if (t0 + u < (uint32_t)T) dst[o + u * vpr.d] = val[u];
   }
 }
 
@@ -1361,10 +1377,13 @@ int skv_gather(const void* k_pool, const void* v_pool, const int32_t* block_tabl
   int64_t blocks = cdiv(total, 256);
   if (blocks > 65535) blocks = 65535;
   if (total < ((int64_t)1 << 31)) {
-    const uint32_t per_head = (uint32_t)max_len * (uint32_t)vpr;
-    hipLaunchKernelGGL(gather32_kernel, dim3((uint32_t)blocks, v_pool ? 2 : 1), dim3(256), 0, (hipStream_t)stream,
+    const uint32_t per_head = (uint32_t)cdiv(max_len, kGatherRows) * (uint32_t)vpr;
+    const int64_t groups = (int64_t)batch * num_heads * per_head;
+    int64_t gblocks = cdiv(groups, 256);
+    if (gblocks > 65535) gblocks = 65535;
+    hipLaunchKernelGGL(gather32_kernel, dim3((uint32_t)gblocks, v_pool ? 2 : 1), dim3(256), 0, (hipStream_t)stream,
                        (const uint4*)k_pool, (const uint4*)(v_pool ? v_pool : k_pool), block_tables, table_stride,
-                       lens, (uint4*)k_out, (uint4*)(v_out ? v_out : k_out), (uint32_t)total,
+                       lens, (uint4*)k_out, (uint4*)(v_out ? v_out : k_out), (uint32_t)groups,
                        make_div(per_head * (uint32_t)num_heads), make_div(per_head), make_div((uint32_t)vpr),
                        make_div((uint32_t)block_size), num_heads, num_blocks, max_len);
   } else {

@@ -114,6 +114,25 @@ def test_gather_bit_exact(cuda, dtype, bs):
             assert np.array_equal(raw(ko[b, :, :n]), raw(ref))
 
 
+@pytest.mark.parametrize("bs,tmax", [(5, 29), (16, 29), (16, 2), (3, 31)])
+def test_gather_ragged_lengths_and_invalid_ids(cuda, bs, tmax):
+    """Output lengths that are not a multiple of the kernel's 4-row groups, block sizes that are not
+    a multiple of 4, lengths beyond the output (clamped) and beyond the table row, and block ids
+    outside the pool (zeros), against the oracle."""
+    gen = torch.Generator().manual_seed(bs * 100 + tmax)
+    nb, h, d, maxblk = 64, 2, 32, 7
+    kp, vp = make_pool(gen, nb, bs, h, d, torch.float16, cuda)
+    tables = make_tables(gen, 6, nb, maxblk)
+    tables[1, 1] = -1
+    tables[2, 0] = nb + 3
+    lens = [tmax, 1, min(tmax, 2 * bs + 1), tmax + 5, 0, bs * maxblk + 9]
+    ko, vo = native.gather(kp, vp, tables.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda), tmax)
+    want_k = O.gather(kp.cpu().float().numpy(), tables.numpy(), lens, tmax)
+    want_v = O.gather(vp.cpu().float().numpy(), tables.numpy(), lens, tmax)
+    assert np.array_equal(ko.cpu().float().numpy(), want_k)
+    assert np.array_equal(vo.cpu().float().numpy(), want_v)
+
+
 def test_append_then_gather_round_trip(cuda):
     gen = torch.Generator().manual_seed(4)
     nb, bs, h, d, n = 128, 16, 8, 64, 300
