@@ -81,7 +81,9 @@ enum skv_status {
   SKV_EWORKSPACE = -4  /* workspace missing or smaller than skv_attention_workspace_bytes */
 };
 
-/* Library version string, e.g. "speechkv 0.1.0 gfx950". */
+/* Library version string, e.g. "speechkv 0.3.0 gfx950 src:0123456789abcdef"; the
+ * src field is a hash of the sources, headers and code flags the library was
+ * built from. */
 SKV_API const char* skv_version(void);
 
 /* Message describing the last non-OK return on the calling thread. */

@@ -8,6 +8,8 @@ The library lands next to the Python package that loads it
 from __future__ import annotations
 
 import argparse
+import glob
+import hashlib
 import os
 import shutil
 import subprocess
@@ -22,6 +24,47 @@ OUTPUT = os.path.join(PKG_ROOT, "speech_serving", "libspeechkv.so")
 ARCH = "gfx950"
 
 
+def code_flags(debug: bool = False) -> list:
+    """The code-generation flags of a build (paths and output names excluded)."""
+    return [
+        f"--offload-arch={ARCH}",
+        "-std=c++17",
+        "-O1" if debug else "-O3",
+        "-fPIC",
+        "-shared",
+        # Packed fp32 VALU ops are kept out of every kernel on purpose.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # The first 16 kernel-argument dwords arrive in scalar registers when a
+        # wave starts (the attention kernel puts its address-chain parameters there).
+        "-mllvm", "-amdgpu-kernarg-preload-count=16",
+        "-fvisibility=hidden",
+        "-Wno-unused-parameter",
+    ]
+
+
+def hashed_files() -> list:
+    """Every file whose bytes reach the library: the HIP sources, their headers and the C-ABI header."""
+    files = glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.h")) + \
+        glob.glob(os.path.join(INCLUDE, "*.h"))
+    return sorted(files, key=lambda f: os.path.relpath(f, REPO_ROOT))
+
+
+def source_digest(debug: bool = False) -> str:
+    """SHA-256 (first 16 hex digits) of the sources and code flags a build compiles.
+
+    The build embeds it in skv_version() ("src:<digest>"); the Python binding
+    recomputes it from the checked-out tree and refuses a library built from
+    anything else."""
+    h = hashlib.sha256()
+    for f in hashed_files():
+        h.update(os.path.relpath(f, REPO_ROOT).replace(os.sep, "/").encode() + b"\0")
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+        h.update(b"\0")
+    h.update(" ".join(code_flags(debug)).encode())
+    return h.hexdigest()[:16]
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and os.path.exists(cand):
@@ -34,20 +77,10 @@ def build(debug: bool = False, verbose: bool = False) -> str:
     tmp = OUTPUT + ".tmp"
     cmd = [
         hipcc(),
-        f"--offload-arch={ARCH}",
-        "-std=c++17",
-        "-O1" if debug else "-O3",
-        "-fPIC",
-        "-shared",
-        # Packed fp32 VALU ops are kept out of every kernel on purpose.
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # The first 16 kernel-argument dwords arrive in scalar registers when a
-        # wave starts (the attention kernel puts its address-chain parameters there).
-        "-mllvm", "-amdgpu-kernarg-preload-count=16",
-        "-fvisibility=hidden",
+        *code_flags(debug),
+        f"-DSKV_SOURCE_DIGEST=\"{source_digest(debug)}\"",
         "-I", INCLUDE,
         "-I", CSRC,
-        "-Wno-unused-parameter",
         "-o", tmp,
         *SOURCES,
     ]

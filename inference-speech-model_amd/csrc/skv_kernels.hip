@@ -1318,7 +1318,13 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
 // ---------------------------------------------------------------------------
 extern "C" {
 
-const char* skv_version(void) { return "speechkv 0.2.0 gfx950"; }
+// The build passes SKV_SOURCE_DIGEST: a hash of the sources, headers and code
+// flags this library was compiled from, which the Python binding checks
+// against the checked-out tree before it binds anything.
+#ifndef SKV_SOURCE_DIGEST
+#define SKV_SOURCE_DIGEST "unknown"
+#endif
+const char* skv_version(void) { return "speechkv 0.3.0 gfx950 src:" SKV_SOURCE_DIGEST; }
 
 const char* skv_last_error(void) { return skv::last_error(); }
 

@@ -58,8 +58,47 @@ def library_path() -> str:
     return _LIB_PATH
 
 
+_BUILD_SCRIPT = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "build.py")
+
+
+def expected_digests() -> Optional[Tuple[str, ...]]:
+    """Source digests a library built from this tree carries (release and debug flags), or None when
+    the tree holds no build script and sources to compare with."""
+    if not os.path.exists(_BUILD_SCRIPT):
+        return None
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_speechkv_build", _BUILD_SCRIPT)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    if not mod.hashed_files():
+        return None
+    return mod.source_digest(False), mod.source_digest(True)
+
+
+def library_digest(handle: ctypes.CDLL) -> str:
+    """The src:<digest> field of a loaded library's skv_version()."""
+    v = handle.skv_version().decode()
+    return v.split("src:", 1)[1].split()[0] if "src:" in v else ""
+
+
+def check_library(handle: ctypes.CDLL) -> None:
+    """Raise RuntimeError unless the library was built from the sources in this tree."""
+    want = expected_digests()
+    if want is None:
+        return
+    got = library_digest(handle)
+    if got not in want:
+        raise RuntimeError(
+            f"{_LIB_PATH} was built from other sources (library src:{got or 'none'}, this tree src:{want[0]}); "
+            "rebuild it with `python inference-speech-model_amd/build.py`")
+
+
 def lib() -> ctypes.CDLL:
-    """Load libspeechkv.so (after torch, so it binds to torch's HIP runtime)."""
+    """Load libspeechkv.so (after torch, so it binds to torch's HIP runtime).
+
+    The library must carry the source digest of this tree (see check_library): a
+    binary left over from an earlier version of the kernels is refused."""
     global _lib
     if _lib is not None:
         return _lib
@@ -74,6 +113,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = res
                 fn.argtypes = args
+            check_library(handle)
             _lib = handle
     return _lib
 

@@ -20,7 +20,24 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP GPU (MI355X)")
 
 
+def _library_is_current():
+    """Build libspeechkv.so when none is built; fail the session when the built one does not come
+    from the sources in this tree (a stale binary must never pass the GPU suite)."""
+    from speech_serving import native
+
+    if not os.path.exists(native.library_path()):
+        import build  # inference-speech-model_amd/build.py
+
+        build.build()
+    try:
+        native.lib()
+    except RuntimeError as e:
+        raise pytest.UsageError(f"libspeechkv.so does not match the checked-out sources: {e}") from None
+
+
 def pytest_collection_modifyitems(config, items):
+    if any("gpu" in item.keywords for item in items) or any("abi" in item.nodeid for item in items):
+        _library_is_current()
     if os.path.exists("/dev/kfd"):
         return
     skip = pytest.mark.skip(reason="no GPU on this machine (/dev/kfd absent)")
