@@ -76,7 +76,8 @@ class EncoderBlockManager:
             del self.prefix_hash_table[content_hash]
         if not self._free:
             raise RuntimeError(
-                f"Out of Encoder KV-cache blocks! All {self.num_blocks} blocks are allocated or referenced.")
+                f"encoder KV pool exhausted: no free block among {self.num_blocks} (all are held by "
+                "requests or by cached encoder outputs)")
         blk = self._free.popleft()
         self.ref_counts[blk] = 1
         if content_hash is not None:

@@ -28,21 +28,22 @@ class MemoryGuard:
             return False
         util = (encoder_allocated + decoder_allocated) / total * 100.0
         if util >= self.high_water_mark_pct:
-            logger.warning(f"[HIGH WATER MARK EXCEEDED] Utilization={util:.1f}%")
+            logger.warning("KV block pools at %.1f%% of capacity (admission limit %.1f%%)", util,
+                           self.high_water_mark_pct)
             return True
         return False
 
     def trigger_bulk_eviction_cleanup(self, freed_blocks: int, reason: str = "high_water_mark"):
         self.eviction_events_count += 1
         self.total_freed_blocks_count += freed_blocks
-        logger.info(f"[BULK EVICTION EVENT #{self.eviction_events_count}] reason={reason} freed={freed_blocks}")
+        logger.info("eviction %d (%s): %d blocks returned to the pools", self.eviction_events_count, reason,
+                    freed_blocks)
         if self.enable_periodic_gc and torch.cuda.is_available():
             torch.cuda.empty_cache()
             self.last_empty_cache_time = time.perf_counter()
 
     def log_telemetry(self, active_requests: int, queued_requests: int, encoder_stats: Dict[str, Any],
                       decoder_stats: Dict[str, Any]):
-        logger.info(
-            f"[TELEMETRY] ActiveReqs={active_requests} QueuedReqs={queued_requests} | "
-            f"EncUtil={encoder_stats['utilization_pct']}% DecUtil={decoder_stats['utilization_pct']}% | "
-            f"Evictions={self.eviction_events_count}")
+        logger.info("requests: %d decoding, %d waiting; encoder pool %s%% used, decoder pool %s%% used; "
+                    "%d evictions so far", active_requests, queued_requests, encoder_stats["utilization_pct"],
+                    decoder_stats["utilization_pct"], self.eviction_events_count)
