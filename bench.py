@@ -98,16 +98,20 @@ def copy_calibration(a):
                       "GBps_read_plus_write": round(2 * n / dt / 1e9, 1)}), flush=True)
 
 
-def measured_traffic(a):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary of this exact config, else None."""
+def measured_traffic(a, digest):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary of this exact config, measured
+    with a library built from these exact sources (same src digest), else None."""
     key = (f"fp16/b{a.batch}/h{a.heads}/d{a.head_dim}/bs{a.block_size}/nb{a.pool_blocks}/"
            f"ctx{a.max_ctx}/seed{a.seed}")
     path = os.path.join(ROOT, "profiles", "paged_attention_config2.md")
     if a.chunk or not os.path.exists(path):
         return None
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch=") and line.split("config=")[-1].strip() == key:
-            return int(line.split()[0].split("=")[1])
+        if not line.startswith("traffic_bytes_per_launch="):
+            continue
+        fields = dict(f.split("=", 1) for f in line.split() if "=" in f)
+        if fields.get("config") == key and fields.get("src") == digest:
+            return int(fields["traffic_bytes_per_launch"])
     return None
 
 
@@ -671,6 +675,7 @@ def main():
             "step_launch": f"captured graphs of {nsets} back-to-back steps (one per set), as the decode replays them",
             "rows": "longest-first (the engine's decode batch layout)",
             "chunk_tokens": a.chunk or native.default_chunk_tokens(a.batch, a.heads, a.head_dim, a.max_ctx, dtype),
+            "library": native.version(),
         },
         "roofline": {
             "bound": "hbm",
@@ -678,9 +683,10 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(a),
+            "traffic": measured_traffic(a, native.library_digest(native.lib())),
             "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE per launch, scaled by a known-size copy "
-                              "(profiles/paged_attention_config2.md)",
+                              "(profiles/paged_attention_config2.md), used only when measured with a library "
+                              "of the same source digest (else null)",
             "kernel": "attention_kernel<fp16, D=64, paged> with fused append",
             "avg_launch_us": round(avg_us, 3),
             "algorithmic_bytes_per_launch": int(avg_bytes),

@@ -138,6 +138,26 @@ def _compact(k: torch.Tensor, v: torch.Tensor, keep: torch.Tensor):
     return torch.gather(k, 2, idx).contiguous(), torch.gather(v, 2, idx).contiguous(), lens
 
 
+def _bucket_mask_lens(mask: torch.Tensor, rows: int, width: int, what: str) -> torch.Tensor:
+    """Per-row lengths of the additive masks of the bucketed graph step (graph_decode_buffers.py:520-537):
+    0 over each row's first positions, -10000 beyond. A row masked everywhere is an idle slot; its
+    uniform -10000 cancels in the reference's softmax, which then weighs every position, so its length
+    is the full width. Outside graph capture the masks are checked: values 0 or <= -1000 only, and the
+    kept positions of each row a prefix. Inside a capture nothing can be read back; the masks are the
+    buffers' own, prefix masks by construction."""
+    m = mask.reshape(rows, -1)
+    if m.shape[1] != width:
+        raise ValueError(f"{what}: mask covers {m.shape[1]} positions per slot, expected {width}")
+    keep = m > -1000
+    n = keep.sum(-1)
+    if not torch.cuda.is_current_stream_capturing():
+        if not bool(((m == 0) | (m <= -1000)).all()):
+            raise NotImplementedError(f"{what}: additive bias other than 0 / large-negative masking")
+        if bool((keep.to(torch.int32).cumprod(-1).sum(-1) != n).any()):
+            raise ValueError(f"{what}: the kept positions of each slot must form a prefix")
+    return torch.where(n == 0, torch.full_like(n, width), n).to(torch.int32)
+
+
 def add_norm(x: torch.Tensor, y: Optional[torch.Tensor], norm: nn.LayerNorm) -> Tuple[torch.Tensor, torch.Tensor]:
     """(s, norm(s)) for s = x + y (s = x when y is None): one skv_add_layernorm launch
     on the GPU, the same two torch ops elsewhere."""
@@ -430,16 +450,18 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
                                 g_cross_mask: Optional[torch.Tensor] = None) -> None:
         """One decode step over static per-slot buffers g_self_kv [S, L, 2, H, bucket, D]
         and g_cross_kv [S, L, 2, H, T, D]; masks are additive with -10000 beyond each
-        slot's length (graph_decode_buffers.py:527-537). Writes argmax tokens."""
+        slot's length (graph_decode_buffers.py:527-537), turned into lengths by
+        _bucket_mask_lens (a slot masked everywhere attends over every position, as the
+        reference's softmax does). Writes argmax tokens."""
         x = self._embed(g_token_ids)
         dev = x.device
         if g_attn_mask is not None:
-            self_lens = (g_attn_mask.reshape(max_slots, -1) > -1000).sum(-1).to(torch.int32)
+            self_lens = _bucket_mask_lens(g_attn_mask, max_slots, bucket, "g_attn_mask")
         else:
             self_lens = torch.full((max_slots,), bucket, dtype=torch.int32, device=dev)
         t_enc = g_cross_kv.shape[4]
         if g_cross_mask is not None:
-            cross_lens = (g_cross_mask.reshape(max_slots, -1) > -1000).sum(-1).to(torch.int32)
+            cross_lens = _bucket_mask_lens(g_cross_mask, max_slots, t_enc, "g_cross_mask")
         else:
             cross_lens = torch.full((max_slots,), t_enc, dtype=torch.int32, device=dev)
         pos = g_positions.view(max_slots).clamp(0, bucket - 1)

@@ -276,7 +276,8 @@ class PhaseAwareSpeechScheduler:
                 self.memory_guard.trigger_bulk_eviction_cleanup(freed, reason="high_water_mark_eviction")
             pe, pd = projected()
             if pe >= hwm or pd >= hwm:
-                logger.warning(f"[BACKPRESSURE] projected utilisation {max(pe, pd):.1f}% >= {hwm}%: rejecting")
+                logger.warning(f"request refused: admitting it would fill the KV pools to {max(pe, pd):.1f}% "
+                               f"(limit {hwm}%)")
                 self.rejected_requests_count += 1
                 return None
 
@@ -398,7 +399,7 @@ class PhaseAwareSpeechScheduler:
                     self._setup_request_after_encode(req, hidden, kv_list, full_hash=req.full_input_hash,
                                                      enc_time=time.perf_counter() - t0)
             except Exception as e:  # deterministic cleanup, reference :558-560
-                logger.error(f"Error in ENCODE_PHASE for req {req.id}: {e}", exc_info=True)
+                logger.error(f"request {req.id} failed while encoding: {e}", exc_info=True)
                 if req in self.active_encode:
                     self.active_encode.remove(req)
                 self._complete_request(req, status=RequestPhase.FAILED)
@@ -485,7 +486,7 @@ class PhaseAwareSpeechScheduler:
                 try:
                     toks = self._prefill(part, p, layers, direct)
                 except Exception as e:
-                    logger.error(f"Error in prefill of reqs {[r.id for r in part]}: {e}", exc_info=True)
+                    logger.error(f"batched prefill of requests {[r.id for r in part]} failed: {e}", exc_info=True)
                     for r in part:
                         self.active_encode.remove(r)
                         self._complete_request(r, status=RequestPhase.FAILED)
@@ -575,10 +576,24 @@ class PhaseAwareSpeechScheduler:
         # Batch rows longest-first (evens the attention kernel's per-unit load);
         # results go back to the requests, whose order is kept.
         reqs = sorted(self.active_decode, key=lambda r: -r.decoder_seq_len)
-        try:
-            for r in reqs:  # block-boundary allocation (reference :780-783)
-                if r.decoder_seq_len % bs == 0:
+        # Block-boundary allocation (reference :780-783), one request at a time: a request
+        # that cannot get its next block fails alone and leaves the batch; the others decode.
+        starved = []
+        for r in reqs:
+            if r.decoder_seq_len % bs == 0:
+                try:
                     r.decoder_block_table.append(self.dual_cache.allocate_decoder_block())
+                except RuntimeError as e:
+                    logger.error(f"request {r.id}: no decoder block for position {r.decoder_seq_len}: {e}")
+                    starved.append(r)
+        for r in starved:
+            reqs.remove(r)
+            self._complete_request(r, status=RequestPhase.FAILED)
+        if starved:
+            self.active_decode = [r for r in self.active_decode if r not in starved]
+        if not reqs:
+            return
+        try:
             b = len(reqs)
             maxblk = max(len(r.decoder_block_table) for r in reqs)
             staging = self._staging(b * (maxblk + 4))
@@ -607,7 +622,7 @@ class PhaseAwareSpeechScheduler:
                 logits = self.model.decode_step_paged(ids, kv, cross)
                 toks = native.argmax(logits).tolist()
         except Exception as e:  # the batched step failed: release every request deterministically
-            logger.error(f"Error in DECODE_PHASE: {e}", exc_info=True)
+            logger.error(f"batched decode step failed, releasing its requests: {e}", exc_info=True)
             for r in list(reqs):
                 self._complete_request(r, status=RequestPhase.FAILED)
             self.active_decode = []

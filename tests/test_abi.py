@@ -166,3 +166,11 @@ def test_python_wrapper_refuses_cpu_tensors():
         native.paged_attention(q, pool, pool, tbl, lens, 1, 0.125)
     with pytest.raises(RuntimeError, match="GPU tensor"):
         native.append(q, q, pool, pool, torch.zeros(1, dtype=torch.int64))
+
+
+def test_library_was_built_from_this_tree():
+    # skv_version() carries the digest of the sources and flags the library was compiled from;
+    # the binding refuses a library whose digest is not this tree's.
+    got = native.library_digest(native.lib())
+    assert len(got) == 16 and got in native.expected_digests()
+    assert f"src:{got}" in native.version()

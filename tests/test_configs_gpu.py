@@ -3,18 +3,26 @@
   C3  Whisper-base-shaped decoder (6 layers, d_model 512, 8 heads x 64, fp16), 32 requests whose
       encoder outputs have valid lengths U[500, 1500] (the explicit cross-attention mask of the
       reference, expressed as per-request lengths), 224 greedy tokens, continuous batching with
-      graph-slot reuse (16 slots for 32 requests). Graph decode must give the eager decode's tokens.
+      graph-slot reuse. The scenario runs on 16 slots: 32 requests on 32 slots would never reuse a
+      slot, which the configuration asks for. Graph decode must give the eager decode's tokens.
   C4  Whisper-small-shaped decoder (12 layers, d_model 768, 12 heads x 64, bf16), 64 graph slots with
       batch buckets 1/8/16/32/64, Poisson arrivals (lambda = 4 req/s on a simulated clock) of 200
       requests with output lengths U[16, 448], readback every 4 steps.
-  C5  Whisper-large-v3-shaped decoder layers (d_model 1280, 20 heads x 64, vocab 51866, bf16; 2 of
-      the 32 layers, which does not change the scheduling), 128 graph slots, a burst of 256
-      requests with 1500 encoder positions and 448 tokens each, and a decoder pool smaller than the
-      burst needs, so admission waits for blocks and blocks are recycled.
+  C5  Whisper-large-v3-shaped decoder (all 32 layers, d_model 1280, 20 heads x 64, vocab 51866,
+      bf16), 128 graph slots, a burst of 256 requests with 1500 encoder positions and 448 tokens
+      each, and a decoder pool smaller than the burst needs, so admission waits for blocks and
+      blocks are recycled.
+
+Every scenario also holds four of its requests' greedy tokens to the float64 oracle on the same
+(rounded) weights and encoder K/V, teacher-forced along the GPU's tokens (precision_check.py): the
+GPU logits stay within E = 8 u sqrt(L) rms(logits) of the oracle's (u the dtype's unit roundoff, L
+the layers), and each GPU token is the oracle's argmax or, at a near-tie, within 2E of it. C3 is
+compared over all 224 tokens, C4 and C5 over their first 32.
 
 Random-init weights N(0, 0.02); EOS disabled so every request runs to its length.
 Mirrors the reference's scenario drivers (scripts/evaluate_real_speech.py:774-779 arrivals,
-phase_aware_scheduler.py:654-656 up-front graph blocks).
+phase_aware_scheduler.py:654-656 up-front graph blocks) and its sequential-vs-batched token check
+(test_speech_engine.py:237-298).
 """
 import numpy as np
 import pytest
@@ -27,6 +35,8 @@ from speech_serving.memory_guard import MemoryGuard
 from speech_serving.models import WhisperClassSpeechEncoderDecoderModel
 from speech_serving.phase_aware_scheduler import PhaseAwareSpeechScheduler, RequestPhase
 
+import precision_check as P
+
 pytestmark = pytest.mark.gpu
 
 PROMPT = [50258, 50259, 50359, 50363]
@@ -36,7 +46,20 @@ QUEUE_ALL = MemoryGuard(high_water_mark_pct=1e9)
 
 def model(cuda, layers, d_model, heads, vocab, dtype, seed):
     m = WhisperClassSpeechEncoderDecoderModel(1, layers, heads, d_model, 80, vocab, head_dim=64)
-    return m.init_normal_(0.02, seed=seed).to(cuda, dtype).eval()
+    return m.init_normal_(0.02, seed=seed, draw_device=str(cuda)).to(cuda, dtype).eval()
+
+
+def oracle_check(m, kvs, paths, steps):
+    """Four requests' tokens (paths) against the float64 oracle on the same weights and encoder K/V,
+    with the GPU's eager logits along the same tokens; returns the comparison's statistics."""
+    om = P.oracle_of(m)
+    cross = [[(k.double().cpu().numpy(), v.double().cpu().numpy()) for k, v in kv] for kv in kvs]
+    want = P.oracle_logits_along(om, PROMPT, cross, paths, steps)
+    del om, cross
+    got = P.gpu_logits_along(m, PROMPT, kvs, paths, steps)
+    stats = P.check_tokens(m.dtype, m.num_decoder_layers, want, paths, gpu_logits=got)
+    print("float64 oracle comparison:", stats)
+    return stats
 
 
 def managers(m, cuda, dtype, dec_blocks, enc_blocks=16):
@@ -77,6 +100,9 @@ def test_c3_base_variable_encoder_lengths_graph_matches_eager(cuda):
             assert s.graph_buffers.active_slot_count() == 0
         results[mode] = [r.generated_tokens for r in done]
     assert results["graph"] == results["eager"]
+    # the shortest and the longest encoder outputs, and the first requests
+    pick = list(dict.fromkeys([int(np.argmin(lengths)), int(np.argmax(lengths)), 0, 1, 2]))[:4]
+    oracle_check(m, [kvs[i] for i in pick], [results["graph"][i] for i in pick], 224)
 
 
 def test_c4_small_poisson_arrivals_with_buckets(cuda):
@@ -110,11 +136,17 @@ def test_c4_small_poisson_arrivals_with_buckets(cuda):
     assert all(r.phase == RequestPhase.COMPLETED for r in done)
     assert len(buckets) >= 3, buckets
     assert dec.allocated_block_count == 0 and s.graph_buffers.active_slot_count() == 0
+    first = {}
+    for i, r in enumerate(done):  # request i used encoder output i % 8
+        if len(r.generated_tokens) >= 32 and i % 8 not in first:
+            first[i % 8] = r.generated_tokens
+    keys = sorted(first)[:4]
+    oracle_check(m, [kvs[k] for k in keys], [first[k] for k in keys], 32)
 
 
 def test_c5_large_v3_burst_exhausts_and_recycles_the_pool(cuda):
     dt = torch.bfloat16
-    m = model(cuda, 2, 1280, 20, 51866, dt, seed=5)
+    m = model(cuda, 32, 1280, 20, 51866, dt, seed=5)
     per_req = -(-(len(PROMPT) + 448) // 16)  # 29 blocks reserved up front per graph request
     pool = 128 * per_req + 100               # room for the 128 slots, not for the 256-request burst
     kvs = [encoder_kv(m, cuda, 1500, 500 + i) for i in range(8)]
@@ -137,3 +169,6 @@ def test_c5_large_v3_burst_exhausts_and_recycles_the_pool(cuda):
     for r in done:
         by_kv.setdefault((r.id - done[0].id) % 8, set()).add(tuple(r.generated_tokens))
     assert all(len(v) == 1 for v in by_kv.values())
+    del s, enc, dec
+    torch.cuda.empty_cache()
+    oracle_check(m, kvs[:4], [list(next(iter(by_kv[k]))) for k in range(4)], 32)

@@ -114,3 +114,28 @@ def test_generation_stops_on_eos_with_a_task_prompt(cuda):
     assert r.phase == RequestPhase.COMPLETED
     assert r.generated_tokens[-1] == eos and len(r.generated_tokens) == 3 and eos not in r.generated_tokens[:-1]
     assert enc.allocated_block_count == 0 and dec.allocated_block_count == 0
+
+
+def test_a_block_starved_request_fails_alone(cuda):
+    """Eager decode with a decoder pool one block short: at the block boundary the first request
+    takes the last free block and the second cannot get one. Only the second fails (its blocks
+    go back to the pool); the first decodes on, with the tokens it has when it runs alone."""
+    m = tiny(cuda)
+    gen = torch.Generator().manual_seed(20)
+    mels = [torch.randn(80, 32, generator=gen).to(cuda) for _ in range(2)]
+    prompt = torch.tensor([[1, 2, 3]])
+    s, _, _ = scheduler(m, cuda, max_batch_size=2)
+    s.submit(mels[0], prompt_token_ids=prompt, max_new_tokens=12)
+    alone = s.run_until_done()[0].generated_tokens[:]
+
+    enc = EncoderBlockManager(2, 4, 16, 8, 64, dtype=torch.float32, device=str(cuda))
+    dec = BlockManager(2, 4, 16, 8, 3, dtype=torch.float32, device=str(cuda))  # 2 prompts + 1 spare
+    # admission backpressure off: both requests are admitted into the short pool
+    s = PhaseAwareSpeechScheduler(m, DualCacheManager(enc, dec), MemoryGuard(high_water_mark_pct=1e9),
+                                  device=str(cuda), max_batch_size=2)
+    ids = [s.submit(mel, prompt_token_ids=prompt, max_new_tokens=12) for mel in mels]
+    done = {r.id: r for r in s.run_until_done()}
+    assert done[ids[0]].phase == RequestPhase.COMPLETED and done[ids[0]].generated_tokens == alone
+    assert done[ids[1]].phase == RequestPhase.FAILED
+    assert 0 < len(done[ids[1]].generated_tokens) < 12
+    assert dec.allocated_block_count == 0 and enc.allocated_block_count == 0
