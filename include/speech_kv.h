@@ -218,6 +218,31 @@ SKV_API int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_str
                         void* stream);
 
 /*
+ * skv_paged_attention_noalloc — skv_paged_attention without a workspace argument.
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, hosts that forbid
+ * hipMalloc). Arguments and results are those of skv_paged_attention; the split-K
+ * partials live in a fixed 4 MiB device array inside the library (one per device,
+ * held until the process ends), so the call allocates nothing. A call whose
+ * partials (skv_attention_workspace_bytes) exceed 4 MiB returns SKV_EWORKSPACE.
+ * Every call on one device shares that array: calls that overlap in time on one
+ * device (different streams) race. The first call on a device looks the array's
+ * address up (hipGetSymbolAddress).
+ */
+SKV_API int skv_paged_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
+                        void* k_pool, void* v_pool,
+                        const int32_t* block_tables, int32_t table_stride,
+                        const int32_t* table_rows,
+                        const int32_t* ctx_lens,
+                        const void* k_new, const void* v_new,
+                        int64_t new_stride_b, int64_t new_stride_q, int64_t new_stride_h,
+                        void* out, int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h,
+                        int32_t batch, int32_t q_len, int32_t num_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t block_size, int32_t num_blocks,
+                        int32_t max_ctx, float scale, int32_t causal, int32_t dtype,
+                        int32_t chunk_tokens, void* stream);
+
+/*
  * skv_dense_attention — attention over contiguous K/V.
  *   K/V element (slot s, kv head h, position t, dim d) is at
  *   k[s*kv_stride_s + h*kv_stride_h + t*kv_stride_t + d] (same strides for v).

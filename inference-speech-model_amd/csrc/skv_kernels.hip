@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include <stdarg.h>
@@ -1314,6 +1315,49 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Split-K scratch of skv_paged_attention_noalloc: a fixed device array, so that
+// entry point allocates nothing. Each device holds its own copy for the life of
+// the process; its address on the current device is looked up once per device
+// (hipGetSymbolAddress) and kept. Host code never passes `scratch` itself to a
+// kernel: on the host the name stands for a host-side shadow, not the device
+// copy. Calls on one device share the array, so calls that overlap in time on
+// one device (different streams) race on it.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = (int64_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch` (looked up on the device's first call).
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "scratch: hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(SKV_EINVAL, "scratch: device %d outside the %d devices the library tracks", dev, kMaxScratchDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return fail(e != hipSuccess ? (int)e : SKV_EINVAL, "scratch: hipGetSymbolAddress failed on device %d: %s", dev,
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return SKV_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // C ABI.
 // ---------------------------------------------------------------------------
 extern "C" {
@@ -1617,6 +1661,39 @@ int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   rc = dispatch_attention<true>(dtype, head_dim, p, (hipStream_t)stream);
   if (rc != SKV_OK) return rc;
   return check_launch("skv_paged_attention");
+}
+
+int skv_paged_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
+                                void* k_pool, void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                                const int32_t* table_rows, const int32_t* ctx_lens, const void* k_new,
+                                const void* v_new, int64_t new_stride_b, int64_t new_stride_q, int64_t new_stride_h,
+                                void* out, int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h, int32_t batch,
+                                int32_t q_len, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                int32_t block_size, int32_t num_blocks, int32_t max_ctx, float scale, int32_t causal,
+                                int32_t dtype, int32_t chunk_tokens, void* stream) {
+  // The split-K partials this call needs, worked out as skv_paged_attention does (its own
+  // validation reports malformed arguments below).
+  if (batch > 0 && q_len > 0 && num_heads > 0 && block_size > 0 && table_stride > 0 && max_ctx > 0 &&
+      elt_bytes(dtype) != 0 && supported_d(head_dim)) {
+    const int64_t cap = (int64_t)table_stride * block_size;
+    const int32_t len = max_ctx > cap ? (int32_t)cap : max_ctx;
+    const int32_t chunk =
+        chunk_tokens > 0 ? chunk_tokens : pick_chunk(batch * q_len, num_heads, head_dim, len, dtype);
+    const int64_t need = workspace_bytes((int64_t)batch * q_len, num_heads, head_dim, cdiv(len, chunk));
+    if (need > kScratchBytes)
+      return fail(SKV_EWORKSPACE,
+                  "skv_paged_attention_noalloc: this call needs %lld bytes of split-K partials, more than the %lld "
+                  "bytes of the library's fixed scratch; use skv_paged_attention with a workspace, or larger "
+                  "chunk_tokens", (long long)need, (long long)kScratchBytes);
+  }
+  void* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc != SKV_OK) return rc;
+  return skv_paged_attention(q, q_stride_b, q_stride_q, q_stride_h, k_pool, v_pool, block_tables, table_stride,
+                             table_rows, ctx_lens, k_new, v_new, new_stride_b, new_stride_q, new_stride_h, out,
+                             o_stride_b, o_stride_q, o_stride_h, batch, q_len, num_heads, num_kv_heads, head_dim,
+                             block_size, num_blocks, max_ctx, scale, causal, dtype, chunk_tokens, ws, kScratchBytes,
+                             stream);
 }
 
 int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h, const void* k,

@@ -43,6 +43,10 @@ SIGNATURES = {
                                      _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p,
                                      _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                      _c_i32, _c_i32, _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p]),
+    "skv_paged_attention_noalloc": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p,
+                                             _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p,
+                                             _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                             _c_i32, _c_i32, _c_f, _c_i32, _c_i32, _c_i32, _c_p]),
     "skv_dense_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p,
                                      _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                      _c_f, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p]),
@@ -411,7 +415,7 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                     ctx_lens: torch.Tensor, max_ctx: int, scale: float, causal: bool = False,
                     table_rows: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                     chunk_tokens: int = 0, k_new: Optional[torch.Tensor] = None,
-                    v_new: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    v_new: Optional[torch.Tensor] = None, noalloc: bool = False) -> torch.Tensor:
     """softmax(q K^T * scale) V over each row's paged K/V.
 
     q: [B, H, D] or [B, Q, H, D]; pools [num_blocks, BS, Hkv, D]; block_tables
@@ -420,6 +424,8 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     With k_new/v_new ([B, Q, Hkv, D] or [B, Hkv, D]) the Q newest keys
     (positions ctx_lens[b]-Q .. ctx_lens[b]-1) are appended into the pools
     through the block table in the same launch.
+    With noalloc the call goes through skv_paged_attention_noalloc: split-K partials in the library's
+    fixed per-device scratch (at most 4 MiB), no workspace; pass `out` to allocate nothing at all.
     Reference math: speech_serving/models.py:126-165 and :444-466; append:
     speech_serving/phase_aware_scheduler.py:1004-1010.
     """
@@ -468,15 +474,17 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         if kn4.stride(3) != 1 or vn4.stride(3) != 1 or kn4.stride() != vn4.stride():
             kn4, vn4 = kn4.contiguous(), vn4.contiguous()
         nstr = (kn4.stride(0), kn4.stride(1), kn4.stride(2))
+    args = (q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2), k_pool.data_ptr(), v_pool.data_ptr(),
+            block_tables.data_ptr(), block_tables.stride(0), _ptr(table_rows), ctx_lens.data_ptr(),
+            _ptr(kn4), _ptr(vn4), nstr[0], nstr[1], nstr[2],
+            o4.data_ptr(), o4.stride(0), o4.stride(1), o4.stride(2), bsz, qlen, heads, hkv, d, bs, nb, max_ctx,
+            float(scale), 1 if causal else 0, code, chunk_tokens)
+    if noalloc:
+        _check(lib().skv_paged_attention_noalloc(*args, _stream(q.device)), "skv_paged_attention_noalloc")
+        return out
     need = attention_workspace_bytes(bsz * qlen, heads, d, max_ctx, q4.dtype, chunk_tokens)
     wp, wn = _scratch(need, q.device)
-    rc = lib().skv_paged_attention(
-        q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2), k_pool.data_ptr(), v_pool.data_ptr(),
-        block_tables.data_ptr(), block_tables.stride(0), _ptr(table_rows), ctx_lens.data_ptr(),
-        _ptr(kn4), _ptr(vn4), nstr[0], nstr[1], nstr[2],
-        o4.data_ptr(), o4.stride(0), o4.stride(1), o4.stride(2), bsz, qlen, heads, hkv, d, bs, nb, max_ctx,
-        float(scale), 1 if causal else 0, code, chunk_tokens, wp, wn, _stream(q.device))
-    _check(rc, "skv_paged_attention")
+    _check(lib().skv_paged_attention(*args, wp, wn, _stream(q.device)), "skv_paged_attention")
     return out
 
 
