@@ -19,6 +19,9 @@ x 64, batch 64):
                             gather kernels
   tts_decode                the streaming multi-codebook TTS engine (reference TTS
                             model's default shape, 64 requests x 256 frames)
+  config1_decode            the Whisper-tiny-shaped decoder of config 1 (4 requests x 64 greedy
+                            tokens, fp32): GPU graph and eager decode tokens/s beside the
+                            reference's eager path on the host
   large_v3_decode           end-to-end greedy decode through the scheduler's
                             captured graphs: 32 layers, d_model 1280, vocab
                             51866, N(0, 0.02) weights, 64 requests x 448 tokens,
@@ -27,6 +30,9 @@ x 64, batch 64):
                             256 requests x 448 tokens at t=0, a decoder pool that holds
                             the 128 slots' blocks but not the burst's, so admission waits
                             for freed blocks and recycles them.
+
+Every cpu_baseline block times oracle/cpu_path.py (the reference's eager path restated in float32
+torch) on torch's host threads and records the thread count and the CPU model.
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu-baseline] [--no-large-v3]
     python bench.py --mode copy    # known-size copy for PMC counter scaling
@@ -66,11 +72,12 @@ def parse():
     ap.add_argument("--no-large-v3", action="store_true", help="skip the large-v3 kernel and decode measurements")
     ap.add_argument("--no-decode", action="store_true", help="skip the large-v3 decode (keep its kernel measurements)")
     ap.add_argument("--no-tts", action="store_true", help="skip the streaming TTS engine measurement")
+    ap.add_argument("--no-config1", action="store_true", help="skip the Whisper-tiny config-1 decode")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--decode-tokens", type=int, default=448)
     ap.add_argument("--decode-layers", type=int, default=32)
     ap.add_argument("--no-serving", action="store_true", help="skip the large-v3 256-request serving burst")
-    ap.add_argument("--mode", choices=["attention", "copy", "decode", "serving", "tts"], default="attention",
+    ap.add_argument("--mode", choices=["attention", "copy", "decode", "serving", "tts", "config1"], default="attention",
                     help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling; "
                          "decode: only the large-v3-shaped greedy decode; serving: only the large-v3 serving "
                          "burst; tts: only the streaming TTS engine")
@@ -200,41 +207,61 @@ def paged_sets(torch, native, dev, dtype, batch, heads, d, bs, nb, max_ctx, seed
     return sets
 
 
-def cpu_baseline(s, a, scale, budget_s):
-    """Time the numpy oracle (float64, one thread) on whole config batches."""
-    from threadpoolctl import threadpool_limits
+def host_cpu():
+    """(threads torch uses, CPU model, logical CPUs the OS reports). The threads are torch's own count,
+    i.e. OMP_NUM_THREADS where it is set (the GPU box's share of the host), else every core."""
+    import torch
 
-    from oracle import paged_kv as O
-
-    kp = s.k_pool.float().cpu().numpy()
-    vp = s.v_pool.float().cpu().numpy()
-    q = s.q.float().cpu().numpy()[:, None]
-    tables = s.tables_cpu.numpy()
-    ctx = s.ctx.tolist()
-    knew = s.k_new.float().cpu().numpy()
-    vnew = s.v_new.float().cpu().numpy()
-    nbytes = attention_bytes(ctx, a.heads, a.head_dim, 2, a.block_size) + append_bytes(a.batch, a.heads,
-                                                                                      a.head_dim, 2)
-    passes = 0
-    with threadpool_limits(limits=1):
-        t0 = time.perf_counter()
-        while True:
-            O.append(kp, vp, knew, vnew, s.slots)
-            O.paged_attention(q, kp, vp, tables, ctx, scale)
-            passes += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s:
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
                 break
-    per = el / passes
-    return {
-        "value": round(nbytes / per / 1e9, 4),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{passes} full batches (append + paged attention, B={a.batch}) by the numpy oracle, "
-                  f"{per * 1e3:.1f} ms per batch",
-        "ms_per_step": round(per * 1e3, 3),
-    }
+    except OSError:
+        pass
+    return torch.get_num_threads(), model, os.cpu_count()
+
+
+def baseline_record(value, unit, sample, **extra):
+    threads, model, cpus = host_cpu()
+    return {"value": value, "unit": unit, "cores": threads, "kind": "port", "dtype": "fp32",
+            "cpu_model": model, "host_logical_cpus": cpus,
+            "path": "the reference's eager path restated in float32 torch (oracle/cpu_path.py)",
+            "sample": sample, **extra}
+
+
+def cpu_baseline(s, a, scale, budget_s):
+    """The config-2 step on the host: append + block-table gather into a zero-padded batch + masked
+    attention in float32 torch on torch's threads (oracle/cpu_path.paged_attention_step). value is
+    the GPU workload's algorithmic bytes (fp16 element size) per CPU call time, so the two values
+    compare as the inverse of their times."""
+    import torch
+
+    from oracle import cpu_path as C
+
+    kp = s.k_pool.float().cpu()
+    vp = s.v_pool.float().cpu()
+    q = s.q.float().cpu()
+    kn, vn = s.k_new.float().cpu(), s.v_new.float().cpu()
+    tables = s.tables_cpu.long()
+    ctx = s.ctx.tolist()
+    nbytes = attention_bytes(ctx, a.heads, a.head_dim, 2, a.block_size) + append_write_bytes(a.batch, a.heads,
+                                                                                             a.head_dim, 2)
+    times = []
+    with torch.no_grad():
+        C.paged_attention_step(q, kp, vp, tables, ctx, kn, vn, scale)  # warm-up
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(times) < 10:
+            t0 = time.perf_counter()
+            C.paged_attention_step(q, kp, vp, tables, ctx, kn, vn, scale)
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return baseline_record(round(nbytes / med / 1e9, 4), "GB/s",
+                           f"{len(times)} calls of the whole config-2 batch (B={a.batch}, fused append + gather + "
+                           f"attention), median {med * 1e3:.2f} ms per call",
+                           ms_per_step=round(med * 1e3, 3))
 
 
 def large_v3_kernels(torch, native, dev, a):
@@ -382,7 +409,7 @@ def large_v3_decode(torch, dev, a):
     del sched, dec, enc
     torch.cuda.empty_cache()
     if not a.no_cpu_baseline:
-        res["cpu_baseline"] = decode_cpu_baseline(model, states, WHISPER_DEFAULT_PREFIX_TOKENS, 8.0)
+        res["cpu_baseline"] = decode_cpu_baseline(model, a.seed + 7, b, WHISPER_DEFAULT_PREFIX_TOKENS, 15.0)
     del model
     return res
 
@@ -447,34 +474,35 @@ def large_v3_serving(torch, dev, a):
     return res
 
 
-def decode_cpu_baseline(model, states, prompt, budget_s):
-    """The numpy oracle of the decoder (float64, one thread) decoding one request greedily with its
-    contiguous past, as the reference's eager path does per request: decode tokens/s (the prompt's
-    prefill is not timed). Same weights and encoder states as the GPU decode."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
-
-    from oracle import decoder as D
-
+def decode_cpu_baseline(model, seed, batch, prompt, budget_s, t_enc=1500):
+    """The reference's eager decode on the host at the GPU figure's batch: float32 torch on torch's
+    threads (oracle/cpu_path.EagerDecode), the same weights and the same per-request encoder states
+    (regenerated from the GPU run's seed, projected on the GPU, copied to host float32). Decode
+    tokens/s over the decode steps that fit in budget_s (the prompt's prefill is not timed)."""
     import torch
 
-    with torch.no_grad():  # the encoder K/V are inputs of the decode: projected on the GPU
-        cross = [(k.double().cpu().numpy(), v.double().cpu().numpy()) for k, v in model.project_cross_kv(states)]
-    state = {k: v.float().cpu().numpy() for k, v in model.state_dict().items()}
-    m = D.Model(state, model.num_heads, model.head_dim)
-    del state
-    with threadpool_limits(limits=1):
-        logits, past = m.decode_step(np.asarray([list(prompt)]), None, cross)
-        tokens = 0
-        t0 = time.perf_counter()
-        while time.perf_counter() - t0 < budget_s:
-            t = int(np.argmax(logits[0, -1]))
-            logits, past = m.decode_step(np.asarray([[t]]), past, cross)
-            tokens += 1
-        el = time.perf_counter() - t0
-    return {"value": round(tokens / el, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{tokens} greedy decode tokens of one request (context {len(prompt) + 1}.."
-                      f"{len(prompt) + tokens}, 1500 encoder positions) by the numpy oracle"}
+    from oracle import cpu_path as C
+
+    dev = model.decoder_norm.weight.device
+    dm, layers = model.hidden_dim, model.num_decoder_layers
+    g = torch.Generator(device=dev).manual_seed(seed)
+    shape = (batch, model.num_heads, t_enc, model.head_dim)
+    cross = [(torch.empty(shape), torch.empty(shape)) for _ in range(layers)]
+    with torch.no_grad():
+        for i in range(batch):
+            states = torch.randn(1, t_enc, dm, generator=g, device=dev, dtype=model.dtype)
+            for l, (k, v) in enumerate(model.project_cross_kv(states)):
+                cross[l][0][i].copy_(k[0].float())
+                cross[l][1][i].copy_(v[0].float())
+    dec = C.Decoder(model.state_dict(), model.num_heads, model.head_dim)
+    run = C.EagerDecode(dec, cross, batched=True)
+    with torch.no_grad():
+        _, steps, busy = run.run(prompt, 64, budget_s=budget_s)
+    return baseline_record(round(batch * steps / busy, 3), "tokens/s",
+                           f"{steps} decode steps of {batch} requests (context {len(prompt) + 1}.."
+                           f"{len(prompt) + steps}, {t_enc} encoder positions each, batched as the reference's "
+                           f"eager scheduler batches them), {busy / max(steps, 1) * 1e3:.0f} ms per step",
+                           batch=batch)
 
 
 def tts_decode(torch, dev, a):
@@ -517,7 +545,7 @@ def tts_decode(torch, dev, a):
     decoded = batch * steps
     cpu = None
     if not a.no_cpu_baseline:
-        cpu = tts_cpu_baseline(model, prompt_len, books, vocab, frames, a.seed, 3.0)
+        cpu = tts_cpu_baseline(model, prompt_len, books, vocab, batch, a.seed, 5.0)
     return {"workload": f"StreamingTTSEngine, bf16, {layers} layers, d_model {hidden}, {heads} heads x "
                         f"{hidden // heads}, {books} codebooks x vocab {vocab}, {batch} requests x {frames} frames "
                         f"from {prompt_len}-frame prompts, block size {bs}",
@@ -527,34 +555,96 @@ def tts_decode(torch, dev, a):
             "admission_s": round(t1 - t0, 3), "completed_ok": ok, "cpu_baseline": cpu}
 
 
-def tts_cpu_baseline(model, prompt_len, books, vocab, frames_per_request, seed, budget_s):
-    """The numpy oracle of the TTS model (float64, one thread) decoding requests one at a time, frame by
-    frame with the contiguous past, as the reference engine does per request: decode frames/s over the
-    same context range as the GPU workload (a request restarts from its prompt after its frames)."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def tts_cpu_baseline(model, prompt_len, books, vocab, batch, seed, budget_s):
+    """The reference TTS engine's step on the host: each active request in turn gathers its past from
+    the pool, runs one frame and scatters its new K/V (oracle/cpu_path.tts_step), float32 torch on
+    torch's threads, the GPU run's weights and batch; decode frames/s over the engine steps that fit
+    in budget_s (the prompts' prefill is not timed)."""
+    import torch
 
-    from oracle.tts import TTSModel
+    from oracle import cpu_path as C
 
-    state = {k: v.float().cpu().numpy() for k, v in model.state_dict().items()}
-    m = TTSModel(state, model.num_heads, model.head_dim)
-    rng = np.random.default_rng(seed)
-    frames, busy, requests = 0, 0.0, 0
-    with threadpool_limits(limits=1):
-        while busy < budget_s:
-            logits, past = m.forward(rng.integers(0, vocab, (1, prompt_len, books)))  # prefill, not timed
-            requests += 1
+    m = C.TTSModel(model.state_dict(), model.num_heads, model.head_dim)
+    bs, frames_cap = 16, 256
+    per = -(-(prompt_len + frames_cap) // bs)
+    h, d = model.num_heads, model.head_dim
+    pools = [(torch.zeros(batch * per, bs, h, d), torch.zeros(batch * per, bs, h, d)) for _ in range(m.core.n)]
+    g = torch.Generator().manual_seed(seed)
+    state = []
+    with torch.no_grad():
+        for r in range(batch):  # prefill (not timed): the prompt's K/V into the request's blocks
+            table = list(range(r * per, (r + 1) * per))
+            logits, kv = m.forward(torch.randint(0, vocab, (1, prompt_len, books), generator=g))
+            for (kp, vp), (k, v) in zip(pools, kv):
+                for pos in range(prompt_len):
+                    kp[table[pos // bs], pos % bs] = k[0, :, pos]
+                    vp[table[pos // bs], pos % bs] = v[0, :, pos]
+            state.append([table, prompt_len, logits[0, -1].argmax(-1)])
+        steps, busy = 0, 0.0
+        while busy < budget_s and steps < frames_cap - 1:
             t0 = time.perf_counter()
-            for _ in range(frames_per_request - 1):
-                tok = logits[0, -1].argmax(axis=-1)
-                logits, past = m.forward(tok[None, None], past)
-                frames += 1
-                if time.perf_counter() - t0 + busy >= budget_s:
-                    break
+            for st in state:
+                st[2] = C.tts_step(m, pools, st[0], st[1], st[2][None, None])
+                st[1] += 1
+            steps += 1
             busy += time.perf_counter() - t0
-    return {"value": round(frames / busy, 2), "unit": "frames/s", "cores": 1, "kind": "port",
-            "sample": f"{frames} decode frames over {requests} request(s), context {prompt_len}.."
-                      f"{prompt_len + frames_per_request - 1}, by the numpy oracle"}
+    return baseline_record(round(batch * steps / busy, 2), "frames/s",
+                           f"{steps} engine steps over {batch} requests one at a time (context {prompt_len}.."
+                           f"{prompt_len + steps}), {busy / max(steps, 1) * 1e3:.1f} ms per engine step")
+
+
+def config1_decode(torch, dev, a):
+    """Config 1: the Whisper-tiny-shaped decoder (4 layers, d_model 384, 4 heads x 64, vocab 51865,
+    float32 N(0, 0.02) weights), 4 requests with 1500 N(0,1) encoder positions projected by
+    cross_attn_k/v, 64 greedy tokens each from the 4-token prompt, block size 16: decode tokens/s of
+    the scheduler's graph decode and eager decode on the GPU, and of the reference's eager path on
+    the host (float32 torch, oracle/cpu_path.EagerDecode) with the same weights and encoder K/V."""
+    from speech_serving import (BlockManager, DualCacheManager, EncoderBlockManager, MemoryGuard,
+                                PhaseAwareSpeechScheduler, WhisperClassSpeechEncoderDecoderModel)
+    from speech_serving.phase_aware_scheduler import WHISPER_DEFAULT_PREFIX_TOKENS
+
+    from oracle import cpu_path as C
+
+    L, dm, h, vocab, b, n, t_enc = 4, 384, 4, 51865, 4, 64, 1500
+    model = WhisperClassSpeechEncoderDecoderModel(1, L, h, dm, 80, vocab, head_dim=64)
+    model = model.init_normal_(0.02, seed=a.seed + 1, draw_device=str(dev)).to(dev).eval()
+    g = torch.Generator(device=dev).manual_seed(a.seed + 2)
+    with torch.no_grad():
+        kvs = [model.project_cross_kv(torch.randn(1, t_enc, dm, generator=g, device=dev)) for _ in range(b)]
+    out = {"workload": f"Whisper-tiny-shaped decoder: {L} layers, d_model {dm}, {h} heads x 64, vocab {vocab}, "
+                       f"fp32 N(0,0.02) weights, {b} requests x {n} greedy tokens from the 4-token prompt, {t_enc} "
+                       f"N(0,1) encoder positions projected by cross_attn_k/v, block size 16"}
+    tokens = {}
+    for mode in ("graph", "eager"):
+        dec = BlockManager(L, h, 64, 16, num_blocks=b * 5 + 8, dtype=torch.float32, device=str(dev))
+        enc = EncoderBlockManager(1, h, 64, 16, num_blocks=8, dtype=torch.float32, device=str(dev))
+        kw = dict(graph_decode=True, graph_readback_k=4, graph_direct_encoder_kv=True, graph_max_enc_len=t_enc) \
+            if mode == "graph" else {}
+        best = None
+        for _ in range(2):  # the better of two runs: the first also pays one-time warm-up
+            sched = PhaseAwareSpeechScheduler(model, DualCacheManager(enc, dec), MemoryGuard(high_water_mark_pct=1e9),
+                                              max_batch_size=b, device=str(dev), eos_token_id=-1, **kw)
+            for kv in kvs:
+                sched.submit_encoded(kv, prompt_token_ids=torch.tensor([WHISPER_DEFAULT_PREFIX_TOKENS]),
+                                     max_new_tokens=n)
+            torch.cuda.synchronize()
+            done = sorted(sched.run_until_done(), key=lambda r: r.id)
+            rate = sum(len(r.generated_tokens) - 1 for r in done) / sched.decode_time_s
+            best = rate if best is None else max(best, rate)
+            tokens[mode] = [r.generated_tokens for r in done]
+        out[f"{mode}_decode_tokens_per_s"] = round(best, 1)
+    out["graph_tokens_equal_eager"] = tokens["graph"] == tokens["eager"]
+    if not a.no_cpu_baseline:
+        cross = [[(k.float().cpu(), v.float().cpu()) for k, v in kv] for kv in kvs]
+        run = C.EagerDecode(C.Decoder(model.state_dict(), h, 64), cross)
+        with torch.no_grad():
+            cpu_toks, steps, busy = run.run(WHISPER_DEFAULT_PREFIX_TOKENS, n)
+        out["cpu_tokens_equal_gpu"] = cpu_toks == tokens["eager"]
+        out["cpu_baseline"] = baseline_record(round(b * steps / busy, 2), "tokens/s",
+                                              f"{steps} decode steps of the {b} requests (all {n} tokens)")
+    del model, kvs
+    torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -584,6 +674,10 @@ def main():
     if a.mode == "tts":  # the streaming TTS engine alone
         native.lib()
         print(json.dumps({"tts_decode": tts_decode(torch, dev, a)}))
+        return
+    if a.mode == "config1":  # the Whisper-tiny config-1 decode alone
+        native.lib()
+        print(json.dumps({"config1_decode": config1_decode(torch, dev, a)}))
         return
     dtype = torch.float16
     scale = 1.0 / math.sqrt(a.head_dim)
@@ -710,6 +804,8 @@ def main():
     # freeing several GB of float64 weights.
     if not a.no_tts:
         result["tts_decode"] = tts_decode(torch, dev, a)
+    if not a.no_config1:
+        result["config1_decode"] = config1_decode(torch, dev, a)
     if not a.no_large_v3:
         result.update(large_v3_kernels(torch, native, dev, a))
         result.update(large_v3_append_gather(torch, native, dev, a))
