@@ -17,6 +17,8 @@ x 64, batch 64):
   large_v3_cross_attention  attention over 1500 contiguous encoder positions
   large_v3_append / _gather the standalone append (encoder K/V store) and block-table
                             gather kernels
+  large_v3_prefill_cross_attention  the prompt prefill's cross-attention, 128 requests x q_len
+                            1 / 4 / 16 (multi-query matrix-core kernel for q_len >= 2)
   tts_decode                the streaming multi-codebook TTS engine (reference TTS
                             model's default shape, 64 requests x 256 frames)
   config1_decode            the Whisper-tiny-shaped decoder of config 1 (4 requests x 64 greedy
@@ -77,7 +79,8 @@ def parse():
     ap.add_argument("--decode-tokens", type=int, default=448)
     ap.add_argument("--decode-layers", type=int, default=32)
     ap.add_argument("--no-serving", action="store_true", help="skip the large-v3 256-request serving burst")
-    ap.add_argument("--mode", choices=["attention", "copy", "decode", "serving", "tts", "config1"], default="attention",
+    ap.add_argument("--mode", choices=["attention", "copy", "decode", "serving", "tts", "config1", "prefill"],
+                    default="attention",
                     help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling; "
                          "decode: only the large-v3-shaped greedy decode; serving: only the large-v3 serving "
                          "burst; tts: only the streaming TTS engine")
@@ -316,6 +319,48 @@ def large_v3_kernels(torch, native, dev, a):
         "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
         "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1), "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
     del kvs, fns
+    torch.cuda.empty_cache()
+    return out
+
+
+def large_v3_prefill_cross(torch, native, dev, a):
+    """The prompt prefill's cross-attention at the large-v3 serving shape: 128 requests x q_len prompt
+    tokens against each request's 1500 contiguous encoder positions (bf16, 20 heads x 64, the
+    slot-major g_cross_kv layer slice). q_len >= 2 runs the multi-query matrix-core kernel (K/V read
+    once per request); q_len 1 and the one-query-per-row form of q_len 4 (every query row re-reads
+    its request's K/V, the kernel used for prompts before) run the decode kernel. Bytes: K/V of
+    every request once, plus q and out."""
+    dt, b, h, d, t = torch.bfloat16, 128, 20, 64, 1500
+    kvs = []
+    for i in range(2):  # 2 x 983 MB > the 256 MB last-level cache
+        g = torch.Generator(device=dev).manual_seed(a.seed + 400 + i)
+        kvs.append(torch.randn(b, 2, h, t, d, generator=g, device=dev, dtype=dt))
+    lens = torch.full((b,), t, dtype=torch.int32, device=dev)
+    out = {"shape": "bf16, 20 heads x 64, 128 requests, 1500 encoder positions each (g_cross_kv slot-major layer "
+                    "slice)"}
+    for q_len in (1, 4, 16):
+        g = torch.Generator(device=dev).manual_seed(a.seed + 410 + q_len)
+        q = torch.randn(b, q_len, h, d, generator=g, device=dev, dtype=dt)
+        res = torch.empty_like(q)
+        native.reserve_attention(b * q_len, h, d, t, dt, dev)
+        fns = [lambda kv=kv: native.dense_attention(q, kv[:, 0], kv[:, 1], lens, t, 0.125, out=res) for kv in kvs]
+        us = graph_launch_us(torch, fns, per_fn=4, replays=5)
+        byts = b * (2 * t * h * d * 2 + q_len * 2 * h * d * 2 + 4)
+        out[f"q{q_len}"] = {"avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": byts,
+                            "achieved_GBps": round(byts / (us * 1e-6) / 1e9, 1),
+                            "frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if q_len == 4:  # the same 4 queries as one-query rows (K/V re-read per query)
+            q1 = q.reshape(b * q_len, 1, h, d)
+            r1 = torch.empty_like(q1)
+            slots = torch.arange(b, dtype=torch.int32, device=dev).repeat_interleave(q_len)
+            lens1 = torch.full((b * q_len,), t, dtype=torch.int32, device=dev)
+            native.reserve_attention(b * q_len, h, d, t, dt, dev)
+            fns = [lambda kv=kv: native.dense_attention(q1, kv[:, 0], kv[:, 1], lens1, t, 0.125, slot_ids=slots,
+                                                        out=r1) for kv in kvs]
+            out["q4_one_query_rows_avg_launch_us"] = round(graph_launch_us(torch, fns, per_fn=4, replays=5), 3)
+            torch.cuda.synchronize()
+            out["q4_max_abs_diff_vs_one_query_rows"] = float((res.float() - r1.view_as(res).float()).abs().max())
+    del kvs
     torch.cuda.empty_cache()
     return out
 
@@ -675,6 +720,10 @@ def main():
         native.lib()
         print(json.dumps({"tts_decode": tts_decode(torch, dev, a)}))
         return
+    if a.mode == "prefill":  # the prompt prefill's cross-attention alone
+        native.lib()
+        print(json.dumps({"large_v3_prefill_cross_attention": large_v3_prefill_cross(torch, native, dev, a)}))
+        return
     if a.mode == "config1":  # the Whisper-tiny config-1 decode alone
         native.lib()
         print(json.dumps({"config1_decode": config1_decode(torch, dev, a)}))
@@ -809,6 +858,7 @@ def main():
     if not a.no_large_v3:
         result.update(large_v3_kernels(torch, native, dev, a))
         result.update(large_v3_append_gather(torch, native, dev, a))
+        result["large_v3_prefill_cross_attention"] = large_v3_prefill_cross(torch, native, dev, a)
         if not a.no_decode:
             result["large_v3_decode"] = large_v3_decode(torch, dev, a)
         if not a.no_serving:

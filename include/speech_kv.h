@@ -249,7 +249,9 @@ SKV_API int skv_paged_attention_noalloc(const void* q, int64_t q_stride_b, int64
  *   Row b reads slot slot_ids ? slot_ids[b] : b.
  *   lens  : int32 [B] keys visible to the last query of row b (causal as above).
  * Used for cross-attention over g_cross_kv [S, L, 2, H, T_enc, D] slices and for
- * causal attention over contiguous prompt K/V.
+ * causal attention over contiguous prompt K/V. Non-causal calls with q_len >= 2
+ * (a prompt's cross-attention), head_dim 64 and fp16/bf16 run every 16 queries of
+ * a row against one read of its K/V, with both products on the matrix cores.
  * Reference: models.py:167-203, :468-479, :126-165 (contiguous past).
  */
 SKV_API int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,

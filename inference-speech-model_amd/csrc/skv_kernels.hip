@@ -1154,6 +1154,345 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Multi-query attention over contiguous K/V on the matrix cores (cross-attention
+// of a prompt, q_len >= 2, non-causal, head_dim 64, fp16/bf16).
+//
+// One workgroup of kWaves waves owns one (row, head, tile of 16 queries, key
+// chunk): the tile's queries share every K/V load, so K/V are read once per tile
+// instead of once per query. Per 32 keys a wave runs
+//   S^T[32 keys x 16 q] = K . Q^T   4 x v_mfma_f32_16x16x32 (2 key tiles x 2 dim slabs)
+//   O^T[64 d x 16 q]   += V^T . P^T  4 x v_mfma_f32_16x16x32 (4 dim blocks)
+// with the gfx950 16x16x32 layouts: operand lane l holds row/column l % 16 and
+// 8 contraction elements for lane group g = l / 16; result lane l holds rows
+// 4g .. 4g+3 of column l % 16. The contraction index an element stands for only
+// has to agree between the two operands, so
+//   * K is loaded as it lies (lane: key 16t + l%16, dims 32s + 8g .. +8);
+//   * S^T's result gives lane l the scores of query l%16 for keys 4g+i (tile 0)
+//     and 16+4g+i (tile 1): exactly the 8 keys {K_g} it contributes to P^T;
+//   * V^T needs 8 keys of one dim per lane: each lane loads one 16-byte key row
+//     slice (dims 8 x 16-bit) of key K_g[l%8] and an 8x8 transpose of 16-bit
+//     values across each 8-lane group turns it into one dim x 8 keys.
+// Online softmax per query (base 2), the max over a 32-key step reduced across
+// the 4 lane groups. P enters its product with V in the input dtype: fp16 rounds
+// it once (the row sums then add the rounded values, so the weights stay a convex
+// combination); bf16 adds the product of the rounded remainder, which keeps the
+// weights to ~16 bits.
+// The waves merge through LDS; a split row writes per-query partials that
+// merge_kernel combines.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_16x16x32(const uint4& a, const uint4& b, const f32x4& c) {
+  if constexpr (DT == SKV_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+}
+
+// Two fp32 values rounded to the dtype (to nearest even) and packed, first value in the
+// low half: v_cvt_pk_bf16_f32 / v_cvt_pk_f16 style conversions, no branches.
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const f32x2 f = {a, b};
+  if constexpr (DT == SKV_BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf162v));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2v));
+  }
+}
+template <int DT>
+__device__ __forceinline__ float lo16(uint32_t w) {
+  if constexpr (DT == SKV_BF16) {
+    return bf16_lo(w);
+  } else {
+    return (float)__builtin_bit_cast(half2v, w).x;
+  }
+}
+template <int DT>
+__device__ __forceinline__ float hi16(uint32_t w) {
+  if constexpr (DT == SKV_BF16) {
+    return bf16_hi(w);
+  } else {
+    return (float)__builtin_bit_cast(half2v, w).y;
+  }
+}
+
+// 8x8 transpose of 16-bit values across the 8 lanes of each aligned lane group:
+// lane r holds row r (elements 2w, 2w+1 in dword w, low half first) and ends
+// with column r in the same packing. Three exchange stages (lane xor 4, 2, 1);
+// every lane of the wave must be active.
+__device__ __forceinline__ uint4 transpose8x8_16(uint4 v) {
+  const int r = lane_id() & 7;
+  // lane xor 4: swap the off-diagonal 4x4 blocks (dwords 2,3 of the low lanes
+  // with dwords 0,1 of the high lanes).
+  {
+    const bool hi = (r & 4) != 0;
+    const uint32_t s0 = __float_as_uint(xor_lane<4>(__uint_as_float(hi ? v.x : v.z)));
+    const uint32_t s1 = __float_as_uint(xor_lane<4>(__uint_as_float(hi ? v.y : v.w)));
+    if (hi) {
+      v.x = s0;
+      v.y = s1;
+    } else {
+      v.z = s0;
+      v.w = s1;
+    }
+  }
+  // lane xor 2: swap the off-diagonal 2x2 blocks inside each 4x4 block, for the
+  // dword pairs (x, y) and (z, w).
+  {
+    const bool hi = (r & 2) != 0;
+    const uint32_t s0 = __float_as_uint(xor_lane<2>(__uint_as_float(hi ? v.x : v.y)));
+    const uint32_t s1 = __float_as_uint(xor_lane<2>(__uint_as_float(hi ? v.z : v.w)));
+    if (hi) {
+      v.x = s0;
+      v.z = s1;
+    } else {
+      v.y = s0;
+      v.w = s1;
+    }
+  }
+  // lane xor 1: swap the off-diagonal 16-bit elements of each 2x2 block. One byte
+  // permute per dword: the even lane keeps its low half and takes the partner's low
+  // half as its high half; the odd lane takes the partner's high half as its low half.
+  {
+    // v_perm_b32 selector over the byte pair (partner, own) = bytes 7..4, 3..0.
+    const uint32_t sel = (r & 1) ? 0x03020706u : 0x05040100u;
+    uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t o = __float_as_uint(xor_lane<1>(__uint_as_float(w[k])));
+      w[k] = __builtin_amdgcn_perm(o, w[k], sel);
+    }
+    v = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  return v;
+}
+
+constexpr int kMqQueries = 16;  // queries per tile (the MFMA's N)
+static_assert(kWaves == 4, "mq_attention_kernel: each of the 4 waves finalises one 16-dim block");
+
+// 3 waves per SIMD: the register budget that holds the next step's loads in flight without
+// spilling (4 spills and halves the rate; 2 is no faster).
+template <int DT>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) void
+mq_attention_kernel(AttnParams p, int32_t qtiles) {
+  constexpr int D = 64;
+  constexpr int PSTRIDE = D + kPartPad;
+  __shared__ float s_m[kWaves][kMqQueries];
+  __shared__ float s_l[kWaves][kMqQueries];
+  // Per-wave K/V staging rows during the key loop; the wave merge reuses the space.
+  constexpr int kStageBytes = kWaves * 2 * 32 * (D * 2 + 16);
+  static_assert(kStageBytes >= (int)sizeof(float) * kWaves * kMqQueries * (D + 4), "merge buffer fits the staging");
+  __shared__ __attribute__((aligned(16))) char s_stage[kStageBytes];
+  auto s_acc = reinterpret_cast<float (*)[kMqQueries][D + 4]>(s_stage);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;   // lane group of the MFMA layouts
+  const int n = lane & 15;   // query column (result, P^T) / key or dim row (operands)
+  const int h = (int)(blockIdx.x % (uint32_t)p.heads);
+  const int qt = (int)(blockIdx.x / (uint32_t)p.heads);
+  const int b = blockIdx.y;
+  const int chunk = blockIdx.z;
+  const int kvh = p.group == 1 ? h : h / p.group;
+
+  int len = p.lens[b];
+  len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+  const int qi = qt * kMqQueries + n;  // this lane's query (result layout)
+  const bool q_ok = qi < p.qlen;
+  if (len == 0) {
+    if (chunk == 0 && wave < 4 && q_ok) {  // zero output: lane writes dims 16*wave + 4g .. +4
+      uint2* o = reinterpret_cast<uint2*>(p.o + (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh);
+      o[(16 * wave + 4 * g) / 4] = make_uint2(0u, 0u);
+    }
+    return;
+  }
+  const int nchunks = p.nchunk_max == 1 ? 1 : (len + p.chunk - 1) / p.chunk;
+  if (chunk >= nchunks) return;
+  const int t_begin = chunk * p.chunk;
+  const int t_end = min(t_begin + p.chunk, len);
+
+  // Q^T operand: lane (query n, group g) holds dims 32s + 8g .. +8 for slabs s = 0, 1.
+  uint4 qf[2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    qf[sl] = make_uint4(0u, 0u, 0u, 0u);
+    if (q_ok) qf[sl] = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + sl * 4 + g];
+  }
+
+  const int slot = p.slots ? p.slots[b] : b;
+  const char* kb = reinterpret_cast<const char*>(p.k) + ((int64_t)slot * p.ss + (int64_t)kvh * p.sh) * 16;
+  const char* vb = reinterpret_cast<const char*>(p.v) + ((int64_t)slot * p.ss + (int64_t)kvh * p.sh) * 16;
+  const __amdgpu_buffer_rsrc_t kres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb), (short)0, (int)p.kv_bytes, kBufWord3);
+  const __amdgpu_buffer_rsrc_t vres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb), (short)0, (int)p.kv_bytes, kBufWord3);
+  const uint32_t row_bytes = (uint32_t)p.st * 16u;
+  // V^T operand: this lane takes key K_g[r] (r = lane % 8) of its 8-lane group,
+  // dims 16 db + 8 * ((lane / 8) % 2) .. +8; K_g = {4g .. 4g+3, 16+4g .. 16+4g+3}.
+  const int r8 = lane & 7;
+  const int v_key = (r8 < 4 ? 4 * g + r8 : 16 + 4 * g + (r8 - 4));
+  const int v_col = 8 * ((lane >> 3) & 1) * 2;
+
+  float m = kNegInf, l = 0.f;  // this lane's query n; l sums the keys of this lane group
+  f32x4 acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int STEP = 32;  // keys per MFMA step; waves take steps in turn
+  // Loads read whole 128-byte key rows (8 lanes per row, 8 rows per instruction) and go
+  // through this wave's LDS rows (padded to 144 bytes) to reach the operand layouts: the
+  // operands want 16 different keys in every 16 lanes, which as direct loads would touch
+  // 16 cache lines per pass.
+  constexpr int kRowPad = D * 2 + 16;
+  char* lds_k = s_stage + wave * (2 * STEP * kRowPad);
+  char* lds_v = lds_k + STEP * kRowPad;
+  const int nat_row = lane >> 3, nat_col = (lane & 7) * 16;  // key row / byte column of a load
+  auto load_step = [&](int base, uint4 (&kr)[4], uint4 (&vr)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = base + 8 * i + nat_row;
+      const uint32_t off = key < t_end ? (uint32_t)key * row_bytes + (uint32_t)nat_col : kBufOutOfRange;
+      kr[i] = load_buf(kres, off);
+      vr[i] = load_buf(vres, off);
+    }
+  };
+  auto compute_step = [&](int base, const uint4 (&kr)[4], const uint4 (&vr)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<uint4*>(lds_k + (8 * i + nat_row) * kRowPad + nat_col) = kr[i];
+      *reinterpret_cast<uint4*>(lds_v + (8 * i + nat_row) * kRowPad + nat_col) = vr[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+    // K operand of tile t, slab s: key 16t + n, dims 32s + 8g .. +8.
+    f32x4 sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const char* row = lds_k + (16 * t + n) * kRowPad + 16 * g;
+      sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row), qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row + 64), qf[1], sc[t]);
+    }
+    // V^T input of dim block db: key K_g[lane % 8], dims 16 db + 8 ((lane / 8) % 2) .. +8.
+    uint4 vin[4];
+    {
+      const char* row = lds_v + v_key * kRowPad + v_col;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) vin[db] = *reinterpret_cast<const uint4*>(row + 32 * db);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // Scores of keys base + 16t + 4g + i for query n, masked past the chunk's end.
+    float sv[8];
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = base + 16 * t + 4 * g + i < t_end;
+        sv[4 * t + i] = ok ? sc[t][i] * p.scale_log2 : kNegInf;
+        mx = fmaxf(mx, sv[4 * t + i]);
+      }
+    mx = fmaxf(mx, xor_lane<16>(mx));
+    mx = fmaxf(mx, xor_lane<32>(mx));
+    const float mn = fmaxf(m, mx);
+    const float ref = mn == kNegInf ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - ref);
+    m = mn;
+    l *= alpha;
+    // P^T operand. fp16 rounds P once (unit roundoff 2^-11) and the row sums add the rounded
+    // values; bf16 (2^-8) splits P into a rounded head and the rounded remainder, two products
+    // with the same V^T, so the weights keep ~16 bits and the sums use P itself.
+    uint32_t pw[4], pr[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float p0 = __builtin_amdgcn_exp2f(sv[2 * k] - ref);
+      const float p1 = __builtin_amdgcn_exp2f(sv[2 * k + 1] - ref);
+      const uint32_t w = pack2<DT>(p0, p1);
+      pw[k] = w;
+      if constexpr (DT == SKV_BF16) {
+        pr[k] = pack2<DT>(p0 - lo16<DT>(w), p1 - hi16<DT>(w));
+        l += p0 + p1;
+      } else {
+        l += lo16<DT>(w) + hi16<DT>(w);
+      }
+    }
+    const uint4 pt = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    const uint4 prt = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      acc[db] *= alpha;
+      const uint4 vt = transpose8x8_16(vin[db]);
+      acc[db] = mfma_16x16x32<DT>(vt, pt, acc[db]);
+      if constexpr (DT == SKV_BF16) acc[db] = mfma_16x16x32<DT>(vt, prt, acc[db]);
+    }
+  };
+  // Software pipeline: the next step's loads are in flight while this step computes.
+  const int stride = kWaves * STEP;
+  int s0 = t_begin + wave * STEP;
+  uint4 ka[4], va[4], kb2[4], vb2[4];
+  if (s0 < t_end) load_step(s0, ka, va);
+  while (s0 < t_end) {
+    const int s1 = s0 + stride;
+    if (s1 < t_end) load_step(s1, kb2, vb2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute_step(s0, ka, va);
+    if (s1 >= t_end) break;
+    const int s2 = s1 + stride;
+    if (s2 < t_end) load_step(s2, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    compute_step(s1, kb2, vb2);
+    s0 = s2;
+  }
+  // Row sums over the 4 lane groups (the max is already common to them).
+  l += xor_lane<16>(l);
+  l += xor_lane<32>(l);
+
+  // Merge the waves: wave w then finalises dim block w for the 16 queries. The merge buffer
+  // overlaps the other waves' staging rows, so every wave leaves its key loop first.
+  __syncthreads();
+  if (g == 0) {
+    s_m[wave][n] = m;
+    s_l[wave][n] = l;
+  }
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_acc[wave][n][16 * db + 4 * g + i] = acc[db][i];
+  __syncthreads();
+  if (wave >= 4) return;
+  float M = kNegInf;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][n]);
+  const float ref = M == kNegInf ? 0.f : M;
+  float L = 0.f, A[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const float e = __builtin_amdgcn_exp2f(s_m[w][n] - ref);
+    L += e * s_l[w][n];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) A[i] += e * s_acc[w][n][16 * wave + 4 * g + i];
+  }
+  if (!q_ok) return;
+  const int d0 = 16 * wave + 4 * g;
+  if (nchunks == 1) {
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    uint2* o = reinterpret_cast<uint2*>(p.o + (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh);
+    o[d0 / 4] = make_uint2(pack2<DT>(A[0] * inv, A[1] * inv), pack2<DT>(A[2] * inv, A[3] * inv));
+    return;
+  }
+  const int64_t rh = ((int64_t)b * p.qlen + qi) * p.heads + h;
+  float* rec = p.part + (rh * p.nchunk_max + chunk) * PSTRIDE;
+  *reinterpret_cast<float4*>(rec + kPartPad + d0) = make_float4(A[0], A[1], A[2], A[3]);
+  if (wave == 0 && g == 0) *reinterpret_cast<float2*>(rec) = make_float2(M, L);
+}
+
+// ---------------------------------------------------------------------------
 // Host helpers.
 // ---------------------------------------------------------------------------
 int64_t workspace_bytes(int64_t rows, int64_t heads, int64_t d, int64_t nchunk_max) {
@@ -1718,6 +2057,26 @@ int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   p.kv_bytes = max_len > 0 ? ((int64_t)(max_len - 1) * (p.st < 0 ? -p.st : p.st) + head_dim / epl) * 16 : 16;
   if (p.st < 0) p.kv_bytes = kBufLimit + 1;  // negative key strides take the 64-bit path
   p.slots = slot_ids;
+  // Several non-causal queries per row (a prompt's cross-attention): one workgroup per
+  // tile of 16 queries reads the row's K/V once and runs both products on the matrix cores.
+  if (!p.causal && q_len >= 2 && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
+      p.kv_bytes <= kBufLimit && p.st > 0 && batch <= 65535) {
+    const int32_t qtiles = (int32_t)cdiv(q_len, kMqQueries);
+    const dim3 grid((uint32_t)(num_heads * qtiles), (uint32_t)batch, (uint32_t)p.nchunk_max);
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == SKV_BF16)
+      hipLaunchKernelGGL(mq_attention_kernel<SKV_BF16>, grid, dim3(64 * kWaves), 0, s, p, qtiles);
+    else
+      hipLaunchKernelGGL(mq_attention_kernel<SKV_F16>, grid, dim3(64 * kWaves), 0, s, p, qtiles);
+    if (p.nchunk_max > 1) {
+      const int64_t rh = (int64_t)batch * q_len * num_heads;
+      if (dtype == SKV_BF16)
+        hipLaunchKernelGGL((merge_kernel<SKV_BF16, 64>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, s, p);
+      else
+        hipLaunchKernelGGL((merge_kernel<SKV_F16, 64>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, s, p);
+    }
+    return check_launch("skv_dense_attention");
+  }
   rc = dispatch_attention<false>(dtype, head_dim, p, (hipStream_t)stream);
   if (rc != SKV_OK) return rc;
   return check_launch("skv_dense_attention");

@@ -1,0 +1,96 @@
+"""Multi-query cross-attention (several prompt tokens per row against one read of the row's encoder
+K/V, both products on the matrix cores) through skv_dense_attention, against the float64 oracle.
+
+The reference's prompt prefill runs its cross-attention with seq_len = prompt length
+(speech_serving/models.py:184-202, called from phase_aware_scheduler.py:664-670). Bar: the
+attention bar of the other kernel tests, max |out - oracle| <= 2e-3 + r |oracle| (r the output
+dtype's relative half-ulp). Covered: 2 to 40 queries (one to three 16-query tiles), lengths 0, 1,
+one and two MFMA steps and the full 1500, slot indirection into the slot-major buffer, rows split
+into key chunks (combined by the merge launch), and graph replays against the eager result.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_kv as O
+from speech_serving import native
+
+pytestmark = pytest.mark.gpu
+
+REL = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}
+
+
+def f64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def check(got, want, dtype, what):
+    err = np.abs(f64(got) - want)
+    tol = 2e-3 + REL[dtype] * np.abs(want)
+    assert (err <= tol).all(), f"{what}: max err {err.max():.3e} (dtype {dtype})"
+    return float(err.max())
+
+
+def cross_case(cuda, dtype, qlen, seed, lens, slots, h=4, t=1500, layers=2, layer=1):
+    gen = torch.Generator().manual_seed(seed)
+    s = max(slots) + 1
+    g = torch.randn(s, layers, 2, h, t, 64, generator=gen).to(cuda, dtype)
+    q = torch.randn(len(slots), qlen, h, 64, generator=gen).to(cuda, dtype)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=cuda)
+    slots_t = torch.tensor(slots, dtype=torch.int32, device=cuda)
+    return g, q, lens_t, slots_t, layer
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("qlen", [2, 4, 16, 17, 40])
+def test_multi_query_cross_attention_matches_oracle(cuda, dtype, qlen):
+    lens = [1500, 0, 1, 31, 33, 500, 64, 1499]
+    slots = [3, 0, 5, 1, 1, 2, 4, 0]
+    g, q, lens_t, slots_t, layer = cross_case(cuda, dtype, qlen, 40 + qlen, lens, slots)
+    out = native.dense_attention(q, g[:, layer, 0], g[:, layer, 1], lens_t, 1500, 0.125, slot_ids=slots_t)
+    want = O.dense_attention(f64(q), f64(g[:, layer, 0]), f64(g[:, layer, 1]), lens, 0.125, slot_ids=slots)
+    err = check(out, want, dtype, f"q_len {qlen}")
+    assert np.all(f64(out)[1] == 0.0)  # an empty row gives zeros
+    print(f"q_len {qlen} {dtype}: max err {err:.2e}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_split_rows_merge(cuda, dtype):
+    # One row x 2 heads: too few (row, head) pairs to fill the GPU, so the keys split into chunks
+    # whose per-query partials the merge launch combines.
+    g, q, lens_t, slots_t, layer = cross_case(cuda, dtype, 4, 7, [1437], [0], h=2)
+    rows = q.shape[0] * q.shape[1]
+    assert native.attention_workspace_bytes(rows, 2, 64, 1500, dtype) > 0
+    out = native.dense_attention(q, g[:, layer, 0], g[:, layer, 1], lens_t, 1500, 0.125, slot_ids=slots_t)
+    want = O.dense_attention(f64(q), f64(g[:, layer, 0]), f64(g[:, layer, 1]), [1437], 0.125, slot_ids=[0])
+    check(out, want, dtype, "split rows")
+
+
+def test_graph_replays_equal_eager(cuda):
+    dtype = torch.bfloat16
+    lens = [1500, 700, 3]
+    slots = [2, 0, 1]
+    g, q, lens_t, slots_t, layer = cross_case(cuda, dtype, 4, 11, lens, slots)
+    out = torch.empty_like(q)
+    native.reserve_attention(q.shape[0] * q.shape[1], 4, 64, 1500, dtype, cuda)
+
+    def call():
+        native.dense_attention(q, g[:, layer, 0], g[:, layer, 1], lens_t, 1500, 0.125, slot_ids=slots_t, out=out)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    gen = torch.Generator().manual_seed(12)
+    for _ in range(4):
+        q.copy_(torch.randn(q.shape, generator=gen).to(cuda, dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        call()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, out)
