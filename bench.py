@@ -365,6 +365,37 @@ def large_v3_prefill_cross(torch, native, dev, a):
     return out
 
 
+def large_v3_encoder_attention(torch, native, dev, a):
+    """EncoderAttentionBackend at the large-v3 encoder shape: 1500 queries x 20 heads x 64 of one
+    request attending its 1500 encoder positions in 94 pool blocks of 16 (bf16, non-causal). The
+    multi-query kernel reads the blocks once per 16 queries; the one-query-per-row form (the path
+    this call took before) reads them once per query. Compute-bound: 4 * 1500 * 1500 * 64 * 20 flops."""
+    dt, h, d, t, bs = torch.bfloat16, 20, 64, 1500, 16
+    nblk = -(-t // bs)
+    g = torch.Generator(device=dev).manual_seed(a.seed + 500)
+    kp = torch.randn(4 * nblk, bs, h, d, generator=g, device=dev, dtype=dt)
+    vp = torch.randn(4 * nblk, bs, h, d, generator=g, device=dev, dtype=dt)
+    table = torch.randperm(4 * nblk, generator=torch.Generator().manual_seed(a.seed + 501))[:nblk].tolist()
+    q = torch.randn(1, t, h, d, generator=g, device=dev, dtype=dt)
+    flops = 4 * t * t * d * h
+    tbl = torch.tensor([table], dtype=torch.int32, device=dev)
+    one = torch.full((1,), t, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    native.reserve_attention(t, h, d, t, dt, dev)
+    # The call EncoderAttentionBackend.forward makes (one shared table row, non-causal).
+    fns = [lambda: native.paged_attention(q, kp, vp, tbl, one, t, 0.125, out=out)]
+    us = graph_launch_us(torch, fns, per_fn=8, replays=5)
+    q1 = q.reshape(t, 1, h, d)
+    rows = torch.zeros(t, dtype=torch.int32, device=dev)
+    lens = torch.full((t,), t, dtype=torch.int32, device=dev)
+    fns1 = [lambda: native.paged_attention(q1, kp, vp, tbl, lens, t, 0.125, table_rows=rows)]
+    us1 = graph_launch_us(torch, fns1, per_fn=4, replays=5)
+    return {"shape": "bf16, one request, 1500 queries x 20 heads x 64 over 1500 positions in 94 pool blocks",
+            "avg_launch_us": round(us, 3), "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+            "frac_of_bf16_mfma_peak": round(flops / (us * 1e-6) / 2.5e15, 4),
+            "one_query_rows_avg_launch_us": round(us1, 3)}
+
+
 def large_v3_append_gather(torch, native, dev, a):
     """Standalone append and block-table gather at Whisper-large-v3 shapes (bf16, 20 heads x 64).
 
@@ -722,7 +753,8 @@ def main():
         return
     if a.mode == "prefill":  # the prompt prefill's cross-attention alone
         native.lib()
-        print(json.dumps({"large_v3_prefill_cross_attention": large_v3_prefill_cross(torch, native, dev, a)}))
+        print(json.dumps({"large_v3_prefill_cross_attention": large_v3_prefill_cross(torch, native, dev, a),
+                          "large_v3_encoder_attention": large_v3_encoder_attention(torch, native, dev, a)}))
         return
     if a.mode == "config1":  # the Whisper-tiny config-1 decode alone
         native.lib()
@@ -859,6 +891,7 @@ def main():
         result.update(large_v3_kernels(torch, native, dev, a))
         result.update(large_v3_append_gather(torch, native, dev, a))
         result["large_v3_prefill_cross_attention"] = large_v3_prefill_cross(torch, native, dev, a)
+        result["large_v3_encoder_attention"] = large_v3_encoder_attention(torch, native, dev, a)
         if not a.no_decode:
             result["large_v3_decode"] = large_v3_decode(torch, dev, a)
         if not a.no_serving:

@@ -200,7 +200,10 @@ SKV_API int32_t skv_default_chunk_tokens(int32_t rows, int32_t num_heads, int32_
  *              pools at pool[table[pos / block_size], pos % block_size] (the
  *              reference's slot-mapping scatter, phase_aware_scheduler.py:
  *              1004-1010 and :681-690) and attends over them in the same launch.
- * A row with 0 visible keys gets a zero output.
+ * A row with 0 visible keys gets a zero output. Non-causal calls with q_len >= 2 and
+ * no fused append (attention over an encoder table), head_dim 64, fp16/bf16 and a
+ * power-of-two block size of at least 8 run every 16 queries of a row against one
+ * read of its blocks, with both products on the matrix cores.
  * Reference: models.py:126-165, :444-466; scripts/evaluate_paging_variants.py:56-133.
  */
 SKV_API int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,

@@ -1280,7 +1280,10 @@ static_assert(kWaves == 4, "mq_attention_kernel: each of the 4 waves finalises o
 
 // 3 waves per SIMD: the register budget that holds the next step's loads in flight without
 // spilling (4 spills and halves the rate; 2 is no faster).
-template <int DT>
+// PAGED: K/V come from the block pools through the row's table (power-of-two block size of
+// at least 8 keys, so the 8 keys of one load instruction share a block id, read with a
+// scalar load); otherwise from the contiguous [slot, head, T, D] layout.
+template <int DT, bool PAGED>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) void
 mq_attention_kernel(AttnParams p, int32_t qtiles) {
   constexpr int D = 64;
@@ -1327,14 +1330,42 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
     if (q_ok) qf[sl] = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + sl * 4 + g];
   }
 
-  const int slot = p.slots ? p.slots[b] : b;
-  const char* kb = reinterpret_cast<const char*>(p.k) + ((int64_t)slot * p.ss + (int64_t)kvh * p.sh) * 16;
-  const char* vb = reinterpret_cast<const char*>(p.v) + ((int64_t)slot * p.ss + (int64_t)kvh * p.sh) * 16;
+  // Descriptors over the row's (slot, head) span (contiguous) or over the whole pool (paged).
+  const char* kb = reinterpret_cast<const char*>(p.k);
+  const char* vb = reinterpret_cast<const char*>(p.v);
+  uint32_t row_bytes, col_base = 0;
+  const uint32_t* trow = nullptr;
+  if constexpr (PAGED) {
+    row_bytes = (uint32_t)p.row_vecs * 16u;
+    col_base = (uint32_t)kvh * (uint32_t)(D * 2);
+    trow = reinterpret_cast<const uint32_t*>(p.tables + (int64_t)(p.trows ? p.trows[b] : b) * p.tstride);
+  } else {
+    const int slot = p.slots ? p.slots[b] : b;
+    kb += ((int64_t)slot * p.ss + (int64_t)kvh * p.sh) * 16;
+    vb += ((int64_t)slot * p.ss + (int64_t)kvh * p.sh) * 16;
+    row_bytes = (uint32_t)p.st * 16u;
+  }
   const __amdgpu_buffer_rsrc_t kres =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb), (short)0, (int)p.kv_bytes, kBufWord3);
   const __amdgpu_buffer_rsrc_t vres =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb), (short)0, (int)p.kv_bytes, kBufWord3);
-  const uint32_t row_bytes = (uint32_t)p.st * 16u;
+  // Byte offset of key `key` (its row's column base added), out of range past t_end or
+  // behind an invalid block id. key0 is the wave-uniform first key of a load instruction;
+  // blk_ok reports (wave-uniformly) whether those 8 keys have a valid block.
+  auto key_offset = [&](int key0, int key, bool& blk_ok) -> uint32_t {
+    if constexpr (PAGED) {
+      // Clamped to the last key so the table index stays inside the row (which covers max_len).
+      const uint32_t k0 = (uint32_t)__builtin_amdgcn_readfirstlane(min(key0, t_end - 1));
+      const uint32_t blk = trow[k0 >> p.bs_shift];  // wave-uniform: a scalar load
+      blk_ok = blk < (uint32_t)p.nb;
+      return key < t_end && blk_ok
+                 ? (blk * (uint32_t)p.bs + ((uint32_t)key & ((uint32_t)p.bs - 1u))) * row_bytes + col_base
+                 : kBufOutOfRange;
+    } else {
+      blk_ok = true;
+      return key < t_end ? (uint32_t)key * row_bytes : kBufOutOfRange;
+    }
+  };
   // V^T operand: this lane takes key K_g[r] (r = lane % 8) of its 8-lane group,
   // dims 16 db + 8 * ((lane / 8) % 2) .. +8; K_g = {4g .. 4g+3, 16+4g .. 16+4g+3}.
   const int r8 = lane & 7;
@@ -1355,16 +1386,24 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
   char* lds_k = s_stage + wave * (2 * STEP * kRowPad);
   char* lds_v = lds_k + STEP * kRowPad;
   const int nat_row = lane >> 3, nat_col = (lane & 7) * 16;  // key row / byte column of a load
-  auto load_step = [&](int base, uint4 (&kr)[4], uint4 (&vr)[4]) {
+  // Returns the step's valid-key mask (bit j: key base + j lies in a valid block).
+  auto load_step = [&](int base, uint4 (&kr)[4], uint4 (&vr)[4]) -> uint32_t {
+    uint32_t off[4], mask = 0u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = base + 8 * i + nat_row;
-      const uint32_t off = key < t_end ? (uint32_t)key * row_bytes + (uint32_t)nat_col : kBufOutOfRange;
-      kr[i] = load_buf(kres, off);
-      vr[i] = load_buf(vres, off);
+      bool blk_ok;
+      const uint32_t o = key_offset(base + 8 * i, base + 8 * i + nat_row, blk_ok);
+      off[i] = o == kBufOutOfRange ? o : o + (uint32_t)nat_col;
+      mask |= blk_ok ? 0xffu << (8 * i) : 0u;
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kr[i] = load_buf(kres, off[i]);
+      vr[i] = load_buf(vres, off[i]);
+    }
+    return mask;
   };
-  auto compute_step = [&](int base, const uint4 (&kr)[4], const uint4 (&vr)[4]) {
+  auto compute_step = [&](int base, const uint4 (&kr)[4], const uint4 (&vr)[4], uint32_t mask) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       *reinterpret_cast<uint4*>(lds_k + (8 * i + nat_row) * kRowPad + nat_col) = kr[i];
@@ -1394,7 +1433,8 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bool ok = base + 16 * t + 4 * g + i < t_end;
+        const int kk = 16 * t + 4 * g + i;
+        const bool ok = base + kk < t_end && (!PAGED || ((mask >> kk) & 1u));
         sv[4 * t + i] = ok ? sc[t][i] * p.scale_log2 : kNegInf;
         mx = fmaxf(mx, sv[4 * t + i]);
       }
@@ -1436,17 +1476,18 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
   const int stride = kWaves * STEP;
   int s0 = t_begin + wave * STEP;
   uint4 ka[4], va[4], kb2[4], vb2[4];
-  if (s0 < t_end) load_step(s0, ka, va);
+  uint32_t ma = 0u, mb = 0u;
+  if (s0 < t_end) ma = load_step(s0, ka, va);
   while (s0 < t_end) {
     const int s1 = s0 + stride;
-    if (s1 < t_end) load_step(s1, kb2, vb2);
+    if (s1 < t_end) mb = load_step(s1, kb2, vb2);
     __builtin_amdgcn_sched_barrier(0);
-    compute_step(s0, ka, va);
+    compute_step(s0, ka, va, ma);
     if (s1 >= t_end) break;
     const int s2 = s1 + stride;
-    if (s2 < t_end) load_step(s2, ka, va);
+    if (s2 < t_end) ma = load_step(s2, ka, va);
     __builtin_amdgcn_sched_barrier(0);
-    compute_step(s1, kb2, vb2);
+    compute_step(s1, kb2, vb2, mb);
     s0 = s2;
   }
   // Row sums over the 4 lane groups (the max is already common to them).
@@ -1652,6 +1693,24 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
 }
 
 }  // namespace
+
+// The multi-query matrix-core attention (fp16/bf16, head_dim 64) and, for split rows, the merge.
+template <bool PAGED>
+void launch_mq(int32_t dtype, const AttnParams& p, hipStream_t s) {
+  const int32_t qtiles = (int32_t)cdiv(p.qlen, kMqQueries);
+  const dim3 grid((uint32_t)(p.heads * qtiles), (uint32_t)p.batch, (uint32_t)p.nchunk_max);
+  if (dtype == SKV_BF16)
+    hipLaunchKernelGGL((mq_attention_kernel<SKV_BF16, PAGED>), grid, dim3(64 * kWaves), 0, s, p, qtiles);
+  else
+    hipLaunchKernelGGL((mq_attention_kernel<SKV_F16, PAGED>), grid, dim3(64 * kWaves), 0, s, p, qtiles);
+  if (p.nchunk_max > 1) {
+    const int64_t rh = (int64_t)p.batch * p.qlen * p.heads;
+    if (dtype == SKV_BF16)
+      hipLaunchKernelGGL((merge_kernel<SKV_BF16, 64>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((merge_kernel<SKV_F16, 64>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, s, p);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Split-K scratch of skv_paged_attention_noalloc: a fixed device array, so that
@@ -1997,6 +2056,13 @@ int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   p.nb = num_blocks;
   p.row_vecs = (int64_t)num_kv_heads * head_dim / (16 / elt_bytes(dtype));
   p.kv_bytes = (int64_t)num_blocks * block_size * p.row_vecs * 16;
+  // Several non-causal queries per row with no fused append (attention over a whole encoder
+  // table, EncoderAttentionBackend): every 16 queries of a row share one read of its blocks.
+  if (!p.causal && q_len >= 2 && !k_new && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
+      p.kv_bytes <= kBufLimit && p.bs_shift >= 3 && batch <= 65535) {
+    launch_mq<true>(dtype, p, (hipStream_t)stream);
+    return check_launch("skv_paged_attention");
+  }
   rc = dispatch_attention<true>(dtype, head_dim, p, (hipStream_t)stream);
   if (rc != SKV_OK) return rc;
   return check_launch("skv_paged_attention");
@@ -2061,20 +2127,7 @@ int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   // tile of 16 queries reads the row's K/V once and runs both products on the matrix cores.
   if (!p.causal && q_len >= 2 && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
       p.kv_bytes <= kBufLimit && p.st > 0 && batch <= 65535) {
-    const int32_t qtiles = (int32_t)cdiv(q_len, kMqQueries);
-    const dim3 grid((uint32_t)(num_heads * qtiles), (uint32_t)batch, (uint32_t)p.nchunk_max);
-    hipStream_t s = (hipStream_t)stream;
-    if (dtype == SKV_BF16)
-      hipLaunchKernelGGL(mq_attention_kernel<SKV_BF16>, grid, dim3(64 * kWaves), 0, s, p, qtiles);
-    else
-      hipLaunchKernelGGL(mq_attention_kernel<SKV_F16>, grid, dim3(64 * kWaves), 0, s, p, qtiles);
-    if (p.nchunk_max > 1) {
-      const int64_t rh = (int64_t)batch * q_len * num_heads;
-      if (dtype == SKV_BF16)
-        hipLaunchKernelGGL((merge_kernel<SKV_BF16, 64>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, s, p);
-      else
-        hipLaunchKernelGGL((merge_kernel<SKV_F16, 64>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, s, p);
-    }
+    launch_mq<false>(dtype, p, (hipStream_t)stream);
     return check_launch("skv_dense_attention");
   }
   rc = dispatch_attention<false>(dtype, head_dim, p, (hipStream_t)stream);

@@ -6,7 +6,8 @@ The reference's prompt prefill runs its cross-attention with seq_len = prompt le
 attention bar of the other kernel tests, max |out - oracle| <= 2e-3 + r |oracle| (r the output
 dtype's relative half-ulp). Covered: 2 to 40 queries (one to three 16-query tiles), lengths 0, 1,
 one and two MFMA steps and the full 1500, slot indirection into the slot-major buffer, rows split
-into key chunks (combined by the merge launch), and graph replays against the eager result.
+into key chunks (combined by the merge launch), graph replays against the eager result, and the
+same kernel over paged K/V (block tables with row indirection, invalid block ids, grouped KV heads).
 """
 import numpy as np
 import pytest
@@ -94,3 +95,33 @@ def test_graph_replays_equal_eager(cuda):
         call()
         torch.cuda.synchronize()
         assert torch.equal(replayed, out)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("qlen,kv_heads", [(3, 4), (16, 4), (33, 2)])
+def test_multi_query_over_paged_blocks(cuda, dtype, qlen, kv_heads):
+    """Non-causal multi-query attention through block tables (the encoder attention path, the
+    reference's EncoderAttentionBackend, encoder_attention.py:22-71): row indirection, invalid
+    block ids excluded, grouped KV heads, lengths up to the table's capacity."""
+    gen = torch.Generator().manual_seed(60 + qlen)
+    h, bs, nb, maxblk = 4, 16, 300, 94
+    kp = torch.randn(nb, bs, kv_heads, 64, generator=gen).to(cuda, dtype)
+    vp = torch.randn(nb, bs, kv_heads, 64, generator=gen).to(cuda, dtype)
+    tables = torch.randperm(nb, generator=gen)[: 3 * maxblk].view(3, maxblk).to(torch.int32)
+    tables[1, 5] = -1          # an invalid id: its keys drop out of the softmax
+    tables[2, 7] = nb + 3
+    rows = [2, 0, 1, 0]
+    lens = [1504, 1, 700, 33]
+    q = torch.randn(len(rows), qlen, h, 64, generator=gen).to(cuda, dtype)
+    out = native.paged_attention(q, kp, vp, tables.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
+                                 maxblk * bs, 0.125, table_rows=torch.tensor(rows, dtype=torch.int32, device=cuda))
+    # Expected: attention over the keys of valid blocks only (an invalid block's keys are left out).
+    kp64, vp64, tb = f64(kp), f64(vp), tables.numpy()
+    want = np.zeros(q.shape)
+    for i, (r, n) in enumerate(zip(rows, lens)):
+        blocks = [int(tb[r, j // bs]) for j in range(n)]
+        keep = [j for j in range(n) if 0 <= blocks[j] < nb]
+        kk = np.stack([kp64[blocks[j], j % bs] for j in keep]).transpose(1, 0, 2)[None]
+        vv = np.stack([vp64[blocks[j], j % bs] for j in keep]).transpose(1, 0, 2)[None]
+        want[i] = O.attention(f64(q)[i:i + 1], kk, vv, [len(keep)], 0.125)[0]
+    check(out, want, dtype, f"paged q_len {qlen} kv_heads {kv_heads}")
