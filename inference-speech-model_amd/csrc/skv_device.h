@@ -125,13 +125,16 @@ constexpr int kDppXor3 = 0x1B;        // quad_perm [3,2,1,0]: i ^ 3
 constexpr int kDppHalfMirror = 0x141; // i ^ 7 (mirror of each 8-lane half row)
 constexpr int kDppRowMirror = 0x140;  // i ^ 15 (mirror of each 16-lane row)
 
+// A DPP read with no old value to keep (bound_ctrl): the compiler then folds the
+// permute into the instruction that consumes it (one v_add_f32_dpp per
+// reduction step instead of a copy, a v_mov_b32_dpp and the add).
 template <int CTRL> __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
 // Value of lane (lane ^ OFF), all in VALU and with every lane active (a DPP
-// read of a lane that is switched off returns the reader's own value, so no
-// lane-dependent branch may surround these): DPP within 16-lane rows, where
+// read of a lane that is switched off returns zero, so no lane-dependent
+// branch may surround these): DPP within 16-lane rows, where
 // i^4 = (i^3)^7 and i^8 = (i^7)^15 compose two permutes; the gfx950
 // permlane16/32 swaps across rows. A swap of a register with itself returns
 // {even-half copy, odd-half copy} of the 16/32 split, so the partner's value

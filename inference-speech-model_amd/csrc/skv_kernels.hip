@@ -664,8 +664,9 @@ __device__ __forceinline__ void write_out(const AttnParams& p, int64_t o_off, fl
 __device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
 
 // One online-softmax step over N keys per lane group: scores from q.k (lane
-// group sum), masked by ok, then the rescale and the p*v accumulation.
-template <int DT, int LPT, int EPL, int N>
+// group sum), masked by ok when MASK (a trip whose keys are all present skips
+// the selects), then the rescale and the p*v accumulation.
+template <int DT, int LPT, int EPL, int N, bool MASK = true>
 __device__ __forceinline__ void softmax_step(const uint4& qv, const uint4* kr, const uint4* vr, const bool* ok,
                                              float scale_log2, float& m, float& l, float* acc) {
   float sc[N];
@@ -673,7 +674,8 @@ __device__ __forceinline__ void softmax_step(const uint4& qv, const uint4* kr, c
 #pragma unroll
   for (int u = 0; u < N; ++u) {
     const float d = group_sum<LPT>(dot16<DT>(qv, kr[u]));
-    sc[u] = ok[u] ? d * scale_log2 : kNegInf;
+    sc[u] = d * scale_log2;
+    if constexpr (MASK) sc[u] = ok[u] ? sc[u] : kNegInf;
     mx = fmaxf(mx, sc[u]);
   }
   const float ref = (mx == kNegInf) ? 0.f : mx;
@@ -863,7 +865,10 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
   // Fused append of one key: the new key is len - 1; the chunk that holds it
   // (uniform test) scores it in the last wave, and the first head of each KV
-  // group stores it into the pool.
+  // group stores it into the pool. The fast path reads the destination's
+  // table entry before its pool trips (app_raw), so the store at the end of
+  // the wave does not wait for a table read.
+  uint32_t app_raw = ~0u;  // raw table entry; checked where it is used
   auto score_new_key = [&]() {
     if (new_begin >= t_begin && new_begin < t_end && wave == kWaves - 1) {
       if constexpr (PAGED && FAST) {
@@ -876,7 +881,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
       softmax_step<DT, LPT, EPL, 1>(qv, &nk, &nv, ok, p.scale_log2, m, l, acc);
       if (g == 0 && (group == 1 || h % group == 0)) {
         const int bi = FAST ? new_begin >> bs_shift : new_begin / p.bs;
-        const int blk = FAST ? table_block(new_begin) : s_blk[bi - first_blk];
+        const int blk = FAST ? (app_raw < (uint32_t)p.nb ? (int)app_raw : -1) : s_blk[bi - first_blk];
         if (blk >= 0) {
           const int64_t dst = ((int64_t)blk * p.bs + (new_begin - bi * p.bs)) * p.row_vecs + base;
           const_cast<uint4*>(p.k)[dst] = nk;
@@ -952,25 +957,50 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
       // block size and SUB are powers of two with TPI <= block size. A load
       // wholly past pool_end reads the last key's table entry and masks every
       // lane. All table loads of a trip issue before the first use, so the trip
-      // waits for one scalar round trip.
-      auto issue = [&](int s, uint4* kr, uint4* vr, bool* ok) {
-        uint32_t raw[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) raw[u] = trow[min((uint32_t)(s + u * TPI), last_key) >> bs_shift];
-        __builtin_amdgcn_sched_barrier(0);
-        const uint32_t trip_off = ((uint32_t)s & bmask) * row_bytes;
+      // waits for one scalar round trip. A trip whose SUB keys all lie before
+      // pool_end in valid blocks (every trip of a row but its last, unless an
+      // id is invalid) takes a copy of the loads and math without per-lane
+      // masks; the test is on scalar values, so the branch is wave-uniform.
+      auto trip_body = [&](auto clean_c, int s, const uint32_t* raw, uint32_t trip_off) __attribute__((always_inline)) {
+        constexpr bool CLEAN = decltype(clean_c)::value;
+        uint4 kr[U], vr[U];
         uint32_t voff[U];
+        bool ok[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const bool valid = raw[u] < (uint32_t)p.nb && g < pool_end - (s + u * TPI);
           const uint32_t sb = raw[u] * blk_bytes + trip_off + cu_off[u];
-          voff[u] = (lane_off + sb) | (valid ? 0u : kBufOutOfRange);
-          ok[u] = valid;
+          if constexpr (CLEAN) {
+            voff[u] = lane_off + sb;
+            ok[u] = true;
+          } else {
+            const bool valid = raw[u] < (uint32_t)p.nb && g < pool_end - (s + u * TPI);
+            voff[u] = (lane_off + sb) | (valid ? 0u : kBufOutOfRange);
+            ok[u] = valid;
+          }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) kr[u] = load_buf(kres, voff[u]);
 #pragma unroll
         for (int u = 0; u < U; ++u) vr[u] = load_buf(vres, voff[u]);
+        // Keep all 2*U loads in flight before the math: without this fence
+        // the scheduler may sink loads into the math to save registers,
+        // which serialises the memory latency.
+        __builtin_amdgcn_sched_barrier(0);
+        softmax_step<DT, LPT, EPL, U, !CLEAN>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
+      };
+      auto trip = [&](int s) __attribute__((always_inline)) {
+        uint32_t raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) raw[u] = trow[min((uint32_t)(s + u * TPI), last_key) >> bs_shift];
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t trip_off = ((uint32_t)s & bmask) * row_bytes;
+        bool blocks_ok = true;
+#pragma unroll
+        for (int u = 0; u < U; ++u) blocks_ok = blocks_ok && raw[u] < (uint32_t)p.nb;
+        if (blocks_ok && s + SUB <= pool_end)
+          trip_body(std::true_type{}, s, raw, trip_off);
+        else
+          trip_body(std::false_type{}, s, raw, trip_off);
       };
       // No load of this wave is waited for before its first K/V loads issue.
       // The last wave's pool trips are a separate copy of the loop: while the
@@ -985,17 +1015,9 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
             __builtin_amdgcn_global_load_lds((glb_ptr)(p.kn + new_off), (lds_ptr)&s_new[0][0], 16, 0, 0);
             __builtin_amdgcn_global_load_lds((glb_ptr)(p.vn + new_off), (lds_ptr)&s_new[1][0], 16, 0, 0);
           }
+          if (one_new) app_raw = (uint32_t)tbl[new_begin >> bs_shift];
         }
-        for (int s = s0; s < pool_end; s += kWaves * SUB) {
-          uint4 kr[U], vr[U];
-          bool ok[U];
-          issue(s, kr, vr, ok);
-          // Keep all 2*U loads in flight before the math: without this fence
-          // the scheduler may sink loads into the math to save registers,
-          // which serialises the memory latency.
-          __builtin_amdgcn_sched_barrier(0);
-          softmax_step<DT, LPT, EPL, U>(qv, kr, vr, ok, p.scale_log2, m, l, acc);
-        }
+        for (int s = s0; s < pool_end; s += kWaves * SUB) trip(s);
         if constexpr (decltype(last_wave)::value) {
           if (one_new) {
             // The LDS copy has landed once this wave's loads have all completed; wait
@@ -1077,35 +1099,101 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
     }
   }
 
-  merge_groups<LPT, EPL>(m, l, acc);
-
-  // Merge the kWaves wave states through LDS.
-  if (g == 0) {
+  if constexpr (LPT == 8 && EPL == 8) {
+    // Head dim 64 in fp16/bf16: the 8 lane groups (lanes 8g + j, dims 8j .. 8j + 7)
+    // move to their common maximum, then the sums are reduce-scattered rather
+    // than all-reduced: the permlane32 and permlane16 swaps exchange half of
+    // the remaining elements each (a swap of two different registers hands
+    // each half-wave or row the partner's copy of the element it keeps), and a
+    // DPP step within each row the last one, so lane (g, j) ends with dim
+    // 8j + g summed over the groups. Wave 0 then merges the 4 waves with one
+    // dim per lane.
+    float mm = m;
+    max_steps<8>(mm);
+    const float gs = __builtin_amdgcn_exp2f(m - (mm == kNegInf ? 0.f : mm));
+    l *= gs;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) s_acc[wave][j * EPL + e] = acc[e];
-    if (j == 0) {
-      s_ml[wave][0] = m;
+    for (int e = 0; e < 8; ++e) acc[e] *= gs;
+    l += xor_lane<8>(l);
+    l += xor_lane<16>(l);
+    l += xor_lane<32>(l);
+    float r1[4], r2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // lanes 0-31 keep element i, lanes 32-63 element i + 4
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[i]), __float_as_uint(acc[i + 4]), false,
+                                                       false);
+      r1[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // row R of 16 lanes keeps element i + 2R
+      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(r1[i]), __float_as_uint(r1[i + 2]), false,
+                                                       false);
+      r2[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    const bool odd = (lane & 8) != 0;  // lane (g, j) keeps element g
+    const float keep = odd ? r2[1] : r2[0];
+    const float send = odd ? r2[0] : r2[1];
+    const float fin = keep + xor_lane<8>(send);
+    s_acc[wave][8 * j + g] = fin;
+    if (lane == 0) {
+      s_ml[wave][0] = mm;
       s_ml[wave][1] = l;
     }
-  }
-  __syncthreads();
-  if (wave != 0 || g != 0) return;
-  float M = s_ml[0][0], L = s_ml[0][1];
-  float A[EPL];
+    __syncthreads();
+    if (wave != 0) return;
+    float M = kNegInf;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) A[e] = s_acc[0][j * EPL + e];
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_ml[w][0]);
+    const float ref = M == kNegInf ? 0.f : M;
+    float L = 0.f, A = 0.f;
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) merge_state<EPL>(M, L, A, s_ml[w][0], s_ml[w][1], &s_acc[w][j * EPL]);
-
-  if (nchunks == 1) {
-    write_out<DT>(p, o_off, L, A);
+    for (int w = 0; w < kWaves; ++w) {
+      const float ew = __builtin_amdgcn_exp2f(s_ml[w][0] - ref);
+      L += ew * s_ml[w][1];
+      A += ew * s_acc[w][lane];
+    }
+    const int64_t o_row = o_off - j;  // the (row, head)'s first 16-byte vector of the output
+    if (nchunks == 1) {
+      const float r = L > 0.f ? A * (1.f / L) : 0.f;
+      const uint32_t bits = DT == SKV_BF16 ? f32_to_bf16_bits(r) : (pack_half2(r, 0.f) & 0xffffu);
+      reinterpret_cast<uint16_t*>(p.o + o_row)[lane] = (uint16_t)bits;
+      return;
+    }
+    float* rec = p.part + ((int64_t)rh * p.nchunk_max + chunk) * PSTRIDE;
+    rec[kPartPad + lane] = A;
+    if (lane == 0) *reinterpret_cast<float2*>(rec) = make_float2(M, L);
     return;
-  }
-  float* rec = p.part + ((int64_t)rh * p.nchunk_max + chunk) * PSTRIDE;
-  float4* dst = reinterpret_cast<float4*>(rec + kPartPad + j * EPL);
+  } else {
+    merge_groups<LPT, EPL>(m, l, acc);
+
+    // Merge the kWaves wave states through LDS.
+    if (g == 0) {
 #pragma unroll
-  for (int e = 0; e < EPL; e += 4) dst[e / 4] = make_float4(A[e], A[e + 1], A[e + 2], A[e + 3]);
-  if (j == 0) *reinterpret_cast<float2*>(rec) = make_float2(M, L);
+      for (int e = 0; e < EPL; ++e) s_acc[wave][j * EPL + e] = acc[e];
+      if (j == 0) {
+        s_ml[wave][0] = m;
+        s_ml[wave][1] = l;
+      }
+    }
+    __syncthreads();
+    if (wave != 0 || g != 0) return;
+    float M = s_ml[0][0], L = s_ml[0][1];
+    float A[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) A[e] = s_acc[0][j * EPL + e];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) merge_state<EPL>(M, L, A, s_ml[w][0], s_ml[w][1], &s_acc[w][j * EPL]);
+
+    if (nchunks == 1) {
+      write_out<DT>(p, o_off, L, A);
+      return;
+    }
+    float* rec = p.part + ((int64_t)rh * p.nchunk_max + chunk) * PSTRIDE;
+    float4* dst = reinterpret_cast<float4*>(rec + kPartPad + j * EPL);
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4) dst[e / 4] = make_float4(A[e], A[e + 1], A[e + 2], A[e + 3]);
+    if (j == 0) *reinterpret_cast<float2*>(rec) = make_float2(M, L);
+  }
 }
 
 // Combine the per-chunk partials of rows that span more than one chunk.
