@@ -185,8 +185,15 @@ def graph_launch_us(torch, fns, per_fn=8, replays=7):
     with torch.cuda.graph(g):
         for i in range(n):
             fns[i % len(fns)]()
+    # Warm-up replays for at least ~0.2 s of GPU time, so the timed replays see the GPU's
+    # steady-state clocks rather than the ramp after an idle host phase.
     g.replay()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.2:
+        for _ in range(4):
+            g.replay()
+        torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
     per = []
     for _ in range(replays):
