@@ -203,7 +203,9 @@ SKV_API int32_t skv_default_chunk_tokens(int32_t rows, int32_t num_heads, int32_
  * A row with 0 visible keys gets a zero output. Non-causal calls with q_len >= 2 and
  * no fused append (attention over an encoder table), head_dim 64, fp16/bf16 and a
  * power-of-two block size of at least 8 run every 16 queries of a row against one
- * read of its blocks, with both products on the matrix cores.
+ * read of its blocks, with both products on the matrix cores; with 64 or more
+ * queries per row and enough (row, head, 64-query) workgroups to fill the GPU,
+ * every 64 queries share one read of the blocks staged in LDS.
  * Reference: models.py:126-165, :444-466; scripts/evaluate_paging_variants.py:56-133.
  */
 SKV_API int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
@@ -254,7 +256,9 @@ SKV_API int skv_paged_attention_noalloc(const void* q, int64_t q_stride_b, int64
  * Used for cross-attention over g_cross_kv [S, L, 2, H, T_enc, D] slices and for
  * causal attention over contiguous prompt K/V. Non-causal calls with q_len >= 2
  * (a prompt's cross-attention), head_dim 64 and fp16/bf16 run every 16 queries of
- * a row against one read of its K/V, with both products on the matrix cores.
+ * a row against one read of its K/V, with both products on the matrix cores (every
+ * 64 queries, staged in LDS, when rows carry 64 or more queries and the
+ * (row, head, 64-query) workgroups fill the GPU).
  * Reference: models.py:167-203, :468-479, :126-165 (contiguous past).
  */
 SKV_API int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,

@@ -158,6 +158,16 @@ template <int OFF> __device__ __forceinline__ float xor_lane(float x) {
   }
 }
 
+// Workgroup barrier that orders LDS only. __syncthreads() is also a release of
+// global memory, which makes every wave wait for all of its outstanding global
+// loads and stores before the barrier; a loop that stages tiles through LDS
+// while the next tiles' global loads are in flight needs only the LDS order.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Sum over groups of W adjacent lanes (W a power of two <= 64); every lane of
 // a group ends with the same bits. After the quad steps all lanes of a quad
 // (then of an 8-lane half row) hold one value, so the mirrors pair each lane

@@ -1622,6 +1622,252 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
 }
 
 // ---------------------------------------------------------------------------
+// Multi-query attention with many queries per row (encoder attention over a
+// table of encoder blocks, q_len = T; long prompts), fp16/bf16, head_dim 64,
+// non-causal: one workgroup owns 64 queries of one (row, head), 16 per wave, and
+// walks all of the row's keys in 32-key steps staged in LDS for the 4 waves, so
+// K/V are read once per 64 queries (mq_attention_kernel reads them once per 16
+// and its waves split the keys). Each wave runs the same products as
+// mq_attention_kernel on the shared step and keeps its own queries' softmax
+// state over every key, so the waves need no merge. Steps are double-buffered
+// in LDS with one barrier per step that orders LDS only, and every wave keeps
+// the global loads of the next three steps in flight: it loads 8 key rows of K
+// and of V per step (8 lanes per 128-byte row).
+// ---------------------------------------------------------------------------
+constexpr int kMqtQueries = 64;  // queries per workgroup, 16 per wave
+
+template <int DT, bool PAGED>
+__global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p) {
+  static_assert(kWaves * kMqQueries == kMqtQueries, "mqt_attention_kernel: 16 queries per wave");
+  constexpr int D = 64;
+  constexpr int STEP = 32;                       // keys per step, 8 per wave
+  constexpr int kRowPad = D * 2 + 16;            // LDS row of one key: 128 bytes + 16 of padding
+  constexpr int kTileBytes = 2 * STEP * kRowPad; // K rows, then V rows
+  __shared__ __attribute__((aligned(16))) char s_tile[2][kTileBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;  // lane group of the MFMA layouts
+  const int n = lane & 15;  // query column (result, P^T) / key or dim row (operands)
+  const int h = (int)(blockIdx.x % (uint32_t)p.heads);
+  const int qg = (int)(blockIdx.x / (uint32_t)p.heads);
+  const int b = blockIdx.y;
+  const int kvh = p.group == 1 ? h : h / p.group;
+
+  int len = p.lens[b];
+  len = len < 0 ? 0 : (len > p.max_len ? p.max_len : len);
+  const int qi = qg * kMqtQueries + wave * kMqQueries + n;  // this lane's query (result layout)
+  const bool q_ok = qi < p.qlen;
+  if (len == 0) {  // uniform over the workgroup: zero output
+    if (q_ok) {
+      uint2* o = reinterpret_cast<uint2*>(p.o + (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[(16 * db + 4 * g) / 4] = make_uint2(0u, 0u);
+    }
+    return;
+  }
+
+  // Q^T operand: lane (query n, group g) holds dims 32s + 8g .. +8 for slabs s = 0, 1.
+  uint4 qf[2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    qf[sl] = make_uint4(0u, 0u, 0u, 0u);
+    if (q_ok) qf[sl] = p.q[(int64_t)b * p.qsb + (int64_t)qi * p.qsq + (int64_t)h * p.qsh + sl * 4 + g];
+  }
+
+  // Descriptors over the row's (slot, head) span (contiguous) or over the whole pool (paged).
+  const char* kb = reinterpret_cast<const char*>(p.k);
+  const char* vb = reinterpret_cast<const char*>(p.v);
+  uint32_t row_bytes, col_base = 0;
+  const uint32_t* trow = nullptr;
+  if constexpr (PAGED) {
+    row_bytes = (uint32_t)p.row_vecs * 16u;
+    col_base = (uint32_t)kvh * (uint32_t)(D * 2);
+    trow = reinterpret_cast<const uint32_t*>(p.tables + (int64_t)(p.trows ? p.trows[b] : b) * p.tstride);
+  } else {
+    const int slot = p.slots ? p.slots[b] : b;
+    kb += ((int64_t)slot * p.ss + (int64_t)kvh * p.sh) * 16;
+    vb += ((int64_t)slot * p.ss + (int64_t)kvh * p.sh) * 16;
+    row_bytes = (uint32_t)p.st * 16u;
+  }
+  const __amdgpu_buffer_rsrc_t kres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb), (short)0, (int)p.kv_bytes, kBufWord3);
+  const __amdgpu_buffer_rsrc_t vres =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb), (short)0, (int)p.kv_bytes, kBufWord3);
+  // Block id of the 8 keys from key0 (a multiple of 8, wave-uniform): a scalar read of the
+  // table, clamped to the row's last key so the index stays inside the row (which covers
+  // max_len); ~0u (invalid) stands for any id outside the pool.
+  auto block_of = [&](int key0) -> uint32_t {
+    const uint32_t k0 = (uint32_t)__builtin_amdgcn_readfirstlane(min(key0, len - 1));
+    return trow[k0 >> p.bs_shift];
+  };
+  // This wave's share of step st: keys st*32 + 8*wave + (lane >> 3), byte column
+  // 16 * (lane & 7) of each row; past len or behind an invalid block the offset is out
+  // of range and the load returns zeros.
+  const int nat_row = lane >> 3, nat_col = (lane & 7) * 16;
+  auto issue = [&](int st, uint4& kr, uint4& vr) {
+    const int key0 = st * STEP + 8 * wave;
+    const int key = key0 + nat_row;
+    uint32_t off;
+    if constexpr (PAGED) {
+      const uint32_t blk = block_of(key0);
+      off = key < len && blk < (uint32_t)p.nb
+                ? (blk * (uint32_t)p.bs + ((uint32_t)key & ((uint32_t)p.bs - 1u))) * row_bytes + col_base +
+                      (uint32_t)nat_col
+                : kBufOutOfRange;
+    } else {
+      off = key < len ? (uint32_t)key * row_bytes + (uint32_t)nat_col : kBufOutOfRange;
+    }
+    kr = load_buf(kres, off);
+    vr = load_buf(vres, off);
+  };
+  auto stage = [&](int buf, const uint4& kr, const uint4& vr) {
+    char* t = s_tile[buf];
+    *reinterpret_cast<uint4*>(t + (8 * wave + nat_row) * kRowPad + nat_col) = kr;
+    *reinterpret_cast<uint4*>(t + STEP * kRowPad + (8 * wave + nat_row) * kRowPad + nat_col) = vr;
+  };
+  // Keys of step st present in the softmax: bit j for key st*32 + j (wave-uniform).
+  auto present = [&](int st) -> uint32_t {
+    const int base = st * STEP;
+    uint32_t bits = base + STEP <= len ? 0xffffffffu : (base < len ? (1u << (len - base)) - 1u : 0u);
+    if constexpr (PAGED) {
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi)
+        if (block_of(base + 8 * gi) >= (uint32_t)p.nb) bits &= ~(0xffu << (8 * gi));
+    }
+    return bits;
+  };
+
+  // V^T operand: this lane takes key K_g[r] (r = lane % 8) of its 8-lane group,
+  // dims 16 db + 8 * ((lane / 8) % 2) .. +8; K_g = {4g .. 4g+3, 16+4g .. 16+4g+3}.
+  const int r8 = lane & 7;
+  const int v_key = (r8 < 4 ? 4 * g + r8 : 16 + 4 * g + (r8 - 4));
+  const int v_col = 8 * ((lane >> 3) & 1) * 2;
+
+  float m = kNegInf, l = 0.f;  // query n's state; l sums the keys of this lane group
+  f32x4 acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // One step on the staged tile. FULL: all 32 keys present (every step of a row but its
+  // last, unless a block id is invalid), so the scores need no mask.
+  auto compute = [&](int buf, uint32_t bits, auto full_c) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full_c)::value;
+    const char* lds_k = s_tile[buf];
+    const char* lds_v = lds_k + STEP * kRowPad;
+    // K operand of tile t, slab s: key 16t + n, dims 32s + 8g .. +8.
+    f32x4 sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const char* row = lds_k + (16 * t + n) * kRowPad + 16 * g;
+      sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row), qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row + 64), qf[1], sc[t]);
+    }
+    uint4 vin[4];
+    {
+      const char* row = lds_v + v_key * kRowPad + v_col;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) vin[db] = *reinterpret_cast<const uint4*>(row + 32 * db);
+    }
+    // Scores of keys 16t + 4g + i for query n.
+    float sv[8];
+    float mx = kNegInf;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kk = 16 * t + 4 * g + i;
+        sv[4 * t + i] = sc[t][i] * p.scale_log2;
+        if constexpr (!FULL) sv[4 * t + i] = ((bits >> kk) & 1u) ? sv[4 * t + i] : kNegInf;
+        mx = fmaxf(mx, sv[4 * t + i]);
+      }
+    mx = fmaxf(mx, xor_lane<16>(mx));
+    mx = fmaxf(mx, xor_lane<32>(mx));
+    const float mn = fmaxf(m, mx);
+    const float ref = mn == kNegInf ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - ref);
+    // The accumulators are rescaled only when some query's maximum grew (alpha is
+    // exactly 1 for the others): past the first steps most steps skip it.
+    const bool rescale = __builtin_amdgcn_ballot_w64(mn != m) != 0;
+    m = mn;
+    l *= alpha;
+    // P^T operand, as in mq_attention_kernel: fp16 rounds P once and sums the rounded
+    // values; bf16 adds the product of the rounded remainder.
+    uint32_t pw[4], pr[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float p0 = __builtin_amdgcn_exp2f(sv[2 * k] - ref);
+      const float p1 = __builtin_amdgcn_exp2f(sv[2 * k + 1] - ref);
+      const uint32_t w = pack2<DT>(p0, p1);
+      pw[k] = w;
+      if constexpr (DT == SKV_BF16) {
+        pr[k] = pack2<DT>(p0 - lo16<DT>(w), p1 - hi16<DT>(w));
+        l += p0 + p1;
+      } else {
+        l += lo16<DT>(w) + hi16<DT>(w);
+      }
+    }
+    const uint4 pt = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    const uint4 prt = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    if (rescale) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const uint4 vt = transpose8x8_16(vin[db]);
+      acc[db] = mfma_16x16x32<DT>(vt, pt, acc[db]);
+      if constexpr (DT == SKV_BF16) acc[db] = mfma_16x16x32<DT>(vt, prt, acc[db]);
+    }
+  };
+
+  // A ring of kRing register slots: step st's loads live in slot st % kRing from their
+  // issue (kRing - 1 steps ahead) until they are staged into LDS buffer st % 2 during
+  // step st - 1. The loop is unrolled by kRing so every slot index is a constant, and
+  // loads are issued unconditionally (past the row's last step they are out of range
+  // and return zeros without a memory access), so the compiler's wait before staging a
+  // step counts only that step's loads and leaves the later ones in flight.
+  constexpr int kRing = 4;
+  const int nsteps = (len + STEP - 1) / STEP;
+  uint4 kr[kRing], vr[kRing];
+#pragma unroll
+  for (int i = 0; i < kRing; ++i) issue(i, kr[i], vr[i]);
+  stage(0, kr[0], vr[0]);
+  lds_barrier();
+  auto body = [&](int st, auto slot_c) __attribute__((always_inline)) {
+    constexpr int SLOT = decltype(slot_c)::value;  // st % kRing
+    constexpr int NEXT = (SLOT + 1) % kRing;
+    if (st + 1 < nsteps) stage((st + 1) & 1, kr[NEXT], vr[NEXT]);
+    issue(st + kRing, kr[SLOT], vr[SLOT]);
+    const uint32_t bits = present(st);
+    if (bits == 0xffffffffu)
+      compute(st & 1, bits, std::true_type{});
+    else
+      compute(st & 1, bits, std::false_type{});
+    lds_barrier();
+  };
+  for (int st = 0; st < nsteps; st += kRing) {
+    body(st, std::integral_constant<int, 0>{});
+    if (st + 1 >= nsteps) break;
+    body(st + 1, std::integral_constant<int, 1>{});
+    if (st + 2 >= nsteps) break;
+    body(st + 2, std::integral_constant<int, 2>{});
+    if (st + 3 >= nsteps) break;
+    body(st + 3, std::integral_constant<int, 3>{});
+  }
+  // Row sums over the 4 lane groups (the max is common to them).
+  l += xor_lane<16>(l);
+  l += xor_lane<32>(l);
+  if (!q_ok) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint2* o = reinterpret_cast<uint2*>(p.o + (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh);
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+    o[(16 * db + 4 * g) / 4] =
+        make_uint2(pack2<DT>(acc[db][0] * inv, acc[db][1] * inv), pack2<DT>(acc[db][2] * inv, acc[db][3] * inv));
+}
+
+// ---------------------------------------------------------------------------
 // Host helpers.
 // ---------------------------------------------------------------------------
 int64_t workspace_bytes(int64_t rows, int64_t heads, int64_t d, int64_t nchunk_max) {
@@ -1798,6 +2044,23 @@ void launch_mq(int32_t dtype, const AttnParams& p, hipStream_t s) {
     else
       hipLaunchKernelGGL((merge_kernel<SKV_F16, 64>), dim3((uint32_t)cdiv(rh, 4)), dim3(256), 0, s, p);
   }
+}
+
+// Many queries per row on the matrix cores: 64 queries per workgroup over all of the row's keys.
+template <bool PAGED>
+void launch_mqt(int32_t dtype, const AttnParams& p, hipStream_t s) {
+  const dim3 grid((uint32_t)(p.heads * cdiv(p.qlen, kMqtQueries)), (uint32_t)p.batch, 1u);
+  if (dtype == SKV_BF16)
+    hipLaunchKernelGGL((mqt_attention_kernel<SKV_BF16, PAGED>), grid, dim3(64 * kWaves), 0, s, p);
+  else
+    hipLaunchKernelGGL((mqt_attention_kernel<SKV_F16, PAGED>), grid, dim3(64 * kWaves), 0, s, p);
+}
+
+// Whether the 64-query kernel serves a multi-query launch: enough queries per row, and
+// enough (row, head, 64 queries) workgroups to fill the GPU without splitting keys.
+bool use_mqt(const AttnParams& p) {
+  return p.qlen >= kMqtQueries && (int64_t)p.batch * p.heads * cdiv(p.qlen, kMqtQueries) >= device_cu_count() &&
+         (int64_t)p.heads * cdiv(p.qlen, kMqtQueries) <= 0x7fffffff;
 }
 
 // ---------------------------------------------------------------------------
@@ -2148,7 +2411,10 @@ int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   // table, EncoderAttentionBackend): every 16 queries of a row share one read of its blocks.
   if (!p.causal && q_len >= 2 && !k_new && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
       p.kv_bytes <= kBufLimit && p.bs_shift >= 3 && batch <= 65535) {
-    launch_mq<true>(dtype, p, (hipStream_t)stream);
+    if (use_mqt(p))
+      launch_mqt<true>(dtype, p, (hipStream_t)stream);
+    else
+      launch_mq<true>(dtype, p, (hipStream_t)stream);
     return check_launch("skv_paged_attention");
   }
   rc = dispatch_attention<true>(dtype, head_dim, p, (hipStream_t)stream);
@@ -2215,7 +2481,10 @@ int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   // tile of 16 queries reads the row's K/V once and runs both products on the matrix cores.
   if (!p.causal && q_len >= 2 && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
       p.kv_bytes <= kBufLimit && p.st > 0 && batch <= 65535) {
-    launch_mq<false>(dtype, p, (hipStream_t)stream);
+    if (use_mqt(p))
+      launch_mqt<false>(dtype, p, (hipStream_t)stream);
+    else
+      launch_mq<false>(dtype, p, (hipStream_t)stream);
     return check_launch("skv_dense_attention");
   }
   rc = dispatch_attention<false>(dtype, head_dim, p, (hipStream_t)stream);

@@ -8,6 +8,11 @@ dtype's relative half-ulp). Covered: 2 to 40 queries (one to three 16-query tile
 one and two MFMA steps and the full 1500, slot indirection into the slot-major buffer, rows split
 into key chunks (combined by the merge launch), graph replays against the eager result, and the
 same kernel over paged K/V (block tables with row indirection, invalid block ids, grouped KV heads).
+
+With 64 or more queries per row and enough (row, head, 64-query) workgroups to fill the GPU, the launch
+takes the 64-query kernel instead (K/V staged in LDS once per 64 queries, each wave over all keys):
+the last tests cover it at 64 to 257 queries, contiguous and paged, and at the encoder-attention
+shape (1500 queries x 20 heads over 94 blocks).
 """
 import numpy as np
 import pytest
@@ -125,3 +130,54 @@ def test_multi_query_over_paged_blocks(cuda, dtype, qlen, kv_heads):
         vv = np.stack([vp64[blocks[j], j % bs] for j in keep]).transpose(1, 0, 2)[None]
         want[i] = O.attention(f64(q)[i:i + 1], kk, vv, [len(keep)], 0.125)[0]
     check(out, want, dtype, f"paged q_len {qlen} kv_heads {kv_heads}")
+
+
+def mqt_selected(rows, heads, qlen):
+    # The library picks the 64-query kernel when rows * heads * ceil(qlen / 64) reaches the CU count.
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    return qlen >= 64 and rows * heads * ((qlen + 63) // 64) >= cus
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("qlen,rows", [(64, 16), (100, 8), (257, 4)])
+def test_many_queries_contiguous(cuda, dtype, qlen, rows):
+    """64-query tiles over contiguous K/V: lengths 0, 1, partial steps, the full 1500; slot indirection."""
+    h = 20
+    assert mqt_selected(rows, h, qlen)
+    lens = ([1500, 0, 1, 33, 700, 1499, 64, 95] * 2)[:rows]
+    slots = ([3, 0, 5, 1, 1, 2, 4, 0] * 2)[:rows]
+    g, q, lens_t, slots_t, layer = cross_case(cuda, dtype, qlen, 90 + qlen, lens, slots, h=h)
+    out = native.dense_attention(q, g[:, layer, 0], g[:, layer, 1], lens_t, 1500, 0.125, slot_ids=slots_t)
+    want = O.dense_attention(f64(q), f64(g[:, layer, 0]), f64(g[:, layer, 1]), lens, 0.125, slot_ids=slots)
+    err = check(out, want, dtype, f"64-query tiles, q_len {qlen}")
+    assert np.all(f64(out)[1] == 0.0)
+    print(f"q_len {qlen} {dtype}: max err {err:.2e}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("kv_heads", [20, 4])
+def test_encoder_attention_shape_paged(cuda, dtype, kv_heads):
+    """The encoder-attention shape on the 64-query kernel: 1500 queries x 20 heads over one table of 94
+    blocks (row indirection to a shared table row), a second row with an invalid block id and a shorter
+    length, grouped KV heads."""
+    h, bs, nb, maxblk, qlen = 20, 16, 200, 94, 1500
+    gen = torch.Generator().manual_seed(70 + kv_heads)
+    kp = torch.randn(nb, bs, kv_heads, 64, generator=gen).to(cuda, dtype)
+    vp = torch.randn(nb, bs, kv_heads, 64, generator=gen).to(cuda, dtype)
+    tables = torch.randperm(nb, generator=gen)[: 2 * maxblk].view(2, maxblk).to(torch.int32)
+    tables[1, 9] = -1
+    rows, lens = [0, 1], [1500, 1001]
+    assert mqt_selected(len(rows), h, qlen)
+    q = torch.randn(len(rows), qlen, h, 64, generator=gen).to(cuda, dtype)
+    out = native.paged_attention(q, kp, vp, tables.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
+                                 maxblk * bs, 0.125, table_rows=torch.tensor(rows, dtype=torch.int32, device=cuda))
+    kp64, vp64, tb = f64(kp), f64(vp), tables.numpy()
+    want = np.zeros(q.shape)
+    for i, (r, n) in enumerate(zip(rows, lens)):
+        blocks = [int(tb[r, j // bs]) for j in range(n)]
+        keep = [j for j in range(n) if 0 <= blocks[j] < nb]
+        kk = np.stack([kp64[blocks[j], j % bs] for j in keep]).transpose(1, 0, 2)[None]
+        vv = np.stack([vp64[blocks[j], j % bs] for j in keep]).transpose(1, 0, 2)[None]
+        want[i] = O.attention(f64(q)[i:i + 1], kk, vv, [len(keep)], 0.125)[0]
+    err = check(out, want, dtype, f"encoder shape kv_heads {kv_heads}")
+    print(f"encoder shape {dtype} kv_heads {kv_heads}: max err {err:.2e}")
