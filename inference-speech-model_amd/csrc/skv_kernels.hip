@@ -1257,9 +1257,9 @@ __global__ __launch_bounds__(256) void merge_kernel(AttnParams p) {
 //   * K is loaded as it lies (lane: key 16t + l%16, dims 32s + 8g .. +8);
 //   * S^T's result gives lane l the scores of query l%16 for keys 4g+i (tile 0)
 //     and 16+4g+i (tile 1): exactly the 8 keys {K_g} it contributes to P^T;
-//   * V^T needs 8 keys of one dim per lane: each lane loads one 16-byte key row
-//     slice (dims 8 x 16-bit) of key K_g[l%8] and an 8x8 transpose of 16-bit
-//     values across each 8-lane group turns it into one dim x 8 keys.
+//   * V^T needs 8 keys of one dim per lane: the gfx950 transpose load
+//     (ds_read_b64_tr_b16) reads them from the row-major LDS rows of the keys
+//     (vt_operand), two loads of 4 keys per operand.
 // Online softmax per query (base 2), the max over a 32-key step reduced across
 // the 4 lane groups. P enters its product with V in the input dtype: fp16 rounds
 // it once (the row sums then add the rounded values, so the weights stay a convex
@@ -1312,55 +1312,20 @@ __device__ __forceinline__ float hi16(uint32_t w) {
   }
 }
 
-// 8x8 transpose of 16-bit values across the 8 lanes of each aligned lane group:
-// lane r holds row r (elements 2w, 2w+1 in dword w, low half first) and ends
-// with column r in the same packing. Three exchange stages (lane xor 4, 2, 1);
-// every lane of the wave must be active.
-__device__ __forceinline__ uint4 transpose8x8_16(uint4 v) {
-  const int r = lane_id() & 7;
-  // lane xor 4: swap the off-diagonal 4x4 blocks (dwords 2,3 of the low lanes
-  // with dwords 0,1 of the high lanes).
-  {
-    const bool hi = (r & 4) != 0;
-    const uint32_t s0 = __float_as_uint(xor_lane<4>(__uint_as_float(hi ? v.x : v.z)));
-    const uint32_t s1 = __float_as_uint(xor_lane<4>(__uint_as_float(hi ? v.y : v.w)));
-    if (hi) {
-      v.x = s0;
-      v.y = s1;
-    } else {
-      v.z = s0;
-      v.w = s1;
-    }
-  }
-  // lane xor 2: swap the off-diagonal 2x2 blocks inside each 4x4 block, for the
-  // dword pairs (x, y) and (z, w).
-  {
-    const bool hi = (r & 2) != 0;
-    const uint32_t s0 = __float_as_uint(xor_lane<2>(__uint_as_float(hi ? v.x : v.y)));
-    const uint32_t s1 = __float_as_uint(xor_lane<2>(__uint_as_float(hi ? v.z : v.w)));
-    if (hi) {
-      v.x = s0;
-      v.z = s1;
-    } else {
-      v.y = s0;
-      v.w = s1;
-    }
-  }
-  // lane xor 1: swap the off-diagonal 16-bit elements of each 2x2 block. One byte
-  // permute per dword: the even lane keeps its low half and takes the partner's low
-  // half as its high half; the odd lane takes the partner's high half as its low half.
-  {
-    // v_perm_b32 selector over the byte pair (partner, own) = bytes 7..4, 3..0.
-    const uint32_t sel = (r & 1) ? 0x03020706u : 0x05040100u;
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t o = __float_as_uint(xor_lane<1>(__uint_as_float(w[k])));
-      w[k] = __builtin_amdgcn_perm(o, w[k], sel);
-    }
-    v = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-  return v;
+// V^T operand of one 16-dim block straight from row-major LDS rows with the gfx950
+// transpose load ds_read_b64_tr_b16. Within each 16-lane group, element j of lane i's
+// result is element i % 4 of the 8-byte chunk addressed by lane 4j + i / 4 of the group
+// (checked on the GPU). Lane 4kk + q of group g addresses key K_g[kk] (first load) and
+// K_g[4 + kk] (second load), dims 16 db + 4q .. +3, with K_g = {4g .. 4g+3, 16+4g ..
+// 16+4g+3}: lane (g, m) then holds dim 16 db + m of the keys K_g in that order, the k
+// order of the P^T operand. row_a / row_b: this lane's two chunk addresses for db = 0.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 vt_operand(const char* row_a, const char* row_b, int db) {
+  typedef __attribute__((address_space(3))) v4i16* lds_v4;
+  const v4i16 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4)(const_cast<char*>(row_a) + 32 * db));
+  const v4i16 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4)(const_cast<char*>(row_b) + 32 * db));
+  const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+  return make_uint4(ua.x, ua.y, ub.x, ub.y);
 }
 
 constexpr int kMqQueries = 16;  // queries per tile (the MFMA's N)
@@ -1454,11 +1419,10 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
       return key < t_end ? (uint32_t)key * row_bytes : kBufOutOfRange;
     }
   };
-  // V^T operand: this lane takes key K_g[r] (r = lane % 8) of its 8-lane group,
-  // dims 16 db + 8 * ((lane / 8) % 2) .. +8; K_g = {4g .. 4g+3, 16+4g .. 16+4g+3}.
-  const int r8 = lane & 7;
-  const int v_key = (r8 < 4 ? 4 * g + r8 : 16 + 4 * g + (r8 - 4));
-  const int v_col = 8 * ((lane >> 3) & 1) * 2;
+  // V^T operand chunks (vt_operand): lane 4kk + q of group g reads keys K_g[kk] and
+  // K_g[4 + kk], dims 16 db + 4q .. +3.
+  const int vt_key = 4 * g + ((lane & 15) >> 2);
+  const int vt_col = 8 * (lane & 3);
 
   float m = kNegInf, l = 0.f;  // this lane's query n; l sums the keys of this lane group
   f32x4 acc[4];
@@ -1506,12 +1470,13 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
       sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row), qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
       sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row + 64), qf[1], sc[t]);
     }
-    // V^T input of dim block db: key K_g[lane % 8], dims 16 db + 8 ((lane / 8) % 2) .. +8.
-    uint4 vin[4];
+    // V^T operands of the 4 dim blocks, transposed by the loads themselves.
+    uint4 vt[4];
     {
-      const char* row = lds_v + v_key * kRowPad + v_col;
+      const char* row_a = lds_v + vt_key * kRowPad + vt_col;
+      const char* row_b = row_a + 16 * kRowPad;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) vin[db] = *reinterpret_cast<const uint4*>(row + 32 * db);
+      for (int db = 0; db < 4; ++db) vt[db] = vt_operand(row_a, row_b, db);
     }
     __builtin_amdgcn_wave_barrier();
     // Scores of keys base + 16t + 4g + i for query n, masked past the chunk's end.
@@ -1555,9 +1520,8 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       acc[db] *= alpha;
-      const uint4 vt = transpose8x8_16(vin[db]);
-      acc[db] = mfma_16x16x32<DT>(vt, pt, acc[db]);
-      if constexpr (DT == SKV_BF16) acc[db] = mfma_16x16x32<DT>(vt, prt, acc[db]);
+      acc[db] = mfma_16x16x32<DT>(vt[db], pt, acc[db]);
+      if constexpr (DT == SKV_BF16) acc[db] = mfma_16x16x32<DT>(vt[db], prt, acc[db]);
     }
   };
   // Software pipeline: the next step's loads are in flight while this step computes.
@@ -1738,11 +1702,10 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
     return bits;
   };
 
-  // V^T operand: this lane takes key K_g[r] (r = lane % 8) of its 8-lane group,
-  // dims 16 db + 8 * ((lane / 8) % 2) .. +8; K_g = {4g .. 4g+3, 16+4g .. 16+4g+3}.
-  const int r8 = lane & 7;
-  const int v_key = (r8 < 4 ? 4 * g + r8 : 16 + 4 * g + (r8 - 4));
-  const int v_col = 8 * ((lane >> 3) & 1) * 2;
+  // V^T operand chunks (vt_operand): lane 4kk + q of group g reads keys K_g[kk] and
+  // K_g[4 + kk], dims 16 db + 4q .. +3.
+  const int vt_key = 4 * g + ((lane & 15) >> 2);
+  const int vt_col = 8 * (lane & 3);
 
   float m = kNegInf, l = 0.f;  // query n's state; l sums the keys of this lane group
   f32x4 acc[4];
@@ -1763,11 +1726,12 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
       sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row), qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
       sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row + 64), qf[1], sc[t]);
     }
-    uint4 vin[4];
+    uint4 vt[4];
     {
-      const char* row = lds_v + v_key * kRowPad + v_col;
+      const char* row_a = lds_v + vt_key * kRowPad + vt_col;
+      const char* row_b = row_a + 16 * kRowPad;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) vin[db] = *reinterpret_cast<const uint4*>(row + 32 * db);
+      for (int db = 0; db < 4; ++db) vt[db] = vt_operand(row_a, row_b, db);
     }
     // Scores of keys 16t + 4g + i for query n.
     float sv[8];
@@ -1815,9 +1779,8 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
     }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const uint4 vt = transpose8x8_16(vin[db]);
-      acc[db] = mfma_16x16x32<DT>(vt, pt, acc[db]);
-      if constexpr (DT == SKV_BF16) acc[db] = mfma_16x16x32<DT>(vt, prt, acc[db]);
+      acc[db] = mfma_16x16x32<DT>(vt[db], pt, acc[db]);
+      if constexpr (DT == SKV_BF16) acc[db] = mfma_16x16x32<DT>(vt[db], prt, acc[db]);
     }
   };
 
