@@ -23,6 +23,12 @@ __device__ __forceinline__ uint4 load_stream(const uint4* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16-byte streaming store (nontemporal hint): for bulk copies whose destination is not
+// read again by the same kernel.
+__device__ __forceinline__ void store_stream(uint4* p, const uint4& v) {
+  __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4*>(p));
+}
+
 // Element traits: EPL = elements carried by one 16-byte lane load.
 template <int DT> struct Elt;
 template <> struct Elt<SKV_F32> { static constexpr int EPL = 4; };
