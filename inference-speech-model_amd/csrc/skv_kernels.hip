@@ -1593,28 +1593,38 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
 // Multi-query attention with many queries per row (encoder attention over a
 // table of encoder blocks, q_len = T; long prompts), fp16/bf16, head_dim 64,
 // non-causal: one workgroup owns 64 queries of one (row, head), 16 per wave, and
-// walks all of the row's keys in 32-key steps staged in LDS for the 4 waves, so
-// K/V are read once per 64 queries (mq_attention_kernel reads them once per 16
-// and its waves split the keys). Each wave runs the same products as
-// mq_attention_kernel on the shared step and keeps its own queries' softmax
-// state over every key, so the waves need no merge. Steps are double-buffered
-// in LDS with one barrier per step that orders LDS only, and every wave keeps
-// the global loads of the next three steps in flight: it loads 8 key rows of K
-// and of V per step (8 lanes per 128-byte row).
+// walks the row's keys in 32-key steps staged in LDS, so K/V are read once per
+// 64 queries (mq_attention_kernel reads them once per 16). The workgroup is two
+// parts of 4 waves: part 0 takes the first half of the steps, part 1 the second,
+// each wave keeping its 16 queries' softmax state over its part's keys, and part 1
+// hands its state to part 0 through LDS at the end. The split puts 4 waves on each
+// SIMD (a 100-VGPR budget) where one part alone would leave 2: the per-step chain
+// (products, softmax, products) is latency-bound, not issue-bound. Each wave runs
+// the same products as mq_attention_kernel on the shared step. Steps are
+// double-buffered in LDS with one barrier per step that orders LDS only; every
+// wave keeps the next step's global loads in flight (8 key rows of K and of V, 8
+// lanes per 128-byte row) and reads that step's block ids in one batch of scalar
+// loads when it issues them.
 // ---------------------------------------------------------------------------
-constexpr int kMqtQueries = 64;  // queries per workgroup, 16 per wave
+constexpr int kMqtQueries = 64;  // queries per workgroup, 16 per wave of a part
+constexpr int kMqtParts = 2;     // key halves per workgroup
 
 template <int DT, bool PAGED>
-__global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * kWaves * kMqtParts) __attribute__((amdgpu_waves_per_eu(4))) void
+mqt_attention_kernel(AttnParams p) {
   static_assert(kWaves * kMqQueries == kMqtQueries, "mqt_attention_kernel: 16 queries per wave");
+  static_assert(kMqtParts == 2, "mqt_attention_kernel: the end-of-kernel merge is written for two parts");
   constexpr int D = 64;
   constexpr int STEP = 32;                       // keys per step, 8 per wave
   constexpr int kRowPad = D * 2 + 16;            // LDS row of one key: 128 bytes + 16 of padding
   constexpr int kTileBytes = 2 * STEP * kRowPad; // K rows, then V rows
-  __shared__ __attribute__((aligned(16))) char s_tile[2][kTileBytes];
+  __shared__ __attribute__((aligned(16))) char s_tiles[kMqtParts][2][kTileBytes];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave_all = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform
+  const int wave = wave_all & (kWaves - 1);  // query tile
+  const int part = wave_all / kWaves;        // key half
+  char(*s_tile)[kTileBytes] = s_tiles[part];
   const int g = lane >> 4;  // lane group of the MFMA layouts
   const int n = lane & 15;  // query column (result, P^T) / key or dim row (operands)
   const int h = (int)(blockIdx.x % (uint32_t)p.heads);
@@ -1627,7 +1637,7 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
   const int qi = qg * kMqtQueries + wave * kMqQueries + n;  // this lane's query (result layout)
   const bool q_ok = qi < p.qlen;
   if (len == 0) {  // uniform over the workgroup: zero output
-    if (q_ok) {
+    if (q_ok && part == 0) {
       uint2* o = reinterpret_cast<uint2*>(p.o + (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh);
 #pragma unroll
       for (int db = 0; db < 4; ++db) o[(16 * db + 4 * g) / 4] = make_uint2(0u, 0u);
@@ -1662,48 +1672,47 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb), (short)0, (int)p.kv_bytes, kBufWord3);
   const __amdgpu_buffer_rsrc_t vres =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb), (short)0, (int)p.kv_bytes, kBufWord3);
-  // Block id of the 8 keys from key0 (a multiple of 8, wave-uniform): a scalar read of the
-  // table, clamped to the row's last key so the index stays inside the row (which covers
-  // max_len); ~0u (invalid) stands for any id outside the pool.
-  auto block_of = [&](int key0) -> uint32_t {
-    const uint32_t k0 = (uint32_t)__builtin_amdgcn_readfirstlane(min(key0, len - 1));
-    return trow[k0 >> p.bs_shift];
-  };
-  // This wave's share of step st: keys st*32 + 8*wave + (lane >> 3), byte column
-  // 16 * (lane & 7) of each row; past len or behind an invalid block the offset is out
-  // of range and the load returns zeros.
+
+  // This part's steps: [st0, st0 + nsteps) of the row's ceil(len / 32), keys below lim.
+  const int nsteps = ((len + STEP - 1) / STEP + kMqtParts - 1) / kMqtParts;
+  const int st0 = part * nsteps;
+  const int lim = min(len, (st0 + nsteps) * STEP);
+
+  // Issues step st's loads for this wave (keys st*32 + 8*wave + (lane >> 3), byte column
+  // 16 * (lane & 7); at or past lim, or behind an invalid block, the offset is out of
+  // range and the load returns zeros without a memory access) and returns the step's
+  // presence bits: bit j for key st*32 + j in the softmax (wave-uniform). The step's
+  // block ids (one per 8 keys, block size >= 8, clamped to the row's last key so the
+  // index stays inside the row) are read in one batch of scalar loads.
   const int nat_row = lane >> 3, nat_col = (lane & 7) * 16;
-  auto issue = [&](int st, uint4& kr, uint4& vr) {
-    const int key0 = st * STEP + 8 * wave;
-    const int key = key0 + nat_row;
+  auto issue = [&](int st, uint4& kr, uint4& vr) -> uint32_t {
+    const int base = st * STEP;
+    const int key = base + 8 * wave + nat_row;
+    uint32_t bits = base + STEP <= len ? 0xffffffffu : (base < len ? (1u << (len - base)) - 1u : 0u);
     uint32_t off;
     if constexpr (PAGED) {
-      const uint32_t blk = block_of(key0);
-      off = key < len && blk < (uint32_t)p.nb
-                ? (blk * (uint32_t)p.bs + ((uint32_t)key & ((uint32_t)p.bs - 1u))) * row_bytes + col_base +
+      uint32_t blk[4];
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi) blk[gi] = trow[(uint32_t)min(base + 8 * gi, len - 1) >> p.bs_shift];
+      const uint32_t own = trow[(uint32_t)min(base + 8 * wave, len - 1) >> p.bs_shift];
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi)
+        if (blk[gi] >= (uint32_t)p.nb) bits &= ~(0xffu << (8 * gi));
+      off = key < lim && own < (uint32_t)p.nb
+                ? (own * (uint32_t)p.bs + ((uint32_t)key & ((uint32_t)p.bs - 1u))) * row_bytes + col_base +
                       (uint32_t)nat_col
                 : kBufOutOfRange;
     } else {
-      off = key < len ? (uint32_t)key * row_bytes + (uint32_t)nat_col : kBufOutOfRange;
+      off = key < lim ? (uint32_t)key * row_bytes + (uint32_t)nat_col : kBufOutOfRange;
     }
     kr = load_buf(kres, off);
     vr = load_buf(vres, off);
+    return bits;
   };
   auto stage = [&](int buf, const uint4& kr, const uint4& vr) {
     char* t = s_tile[buf];
     *reinterpret_cast<uint4*>(t + (8 * wave + nat_row) * kRowPad + nat_col) = kr;
     *reinterpret_cast<uint4*>(t + STEP * kRowPad + (8 * wave + nat_row) * kRowPad + nat_col) = vr;
-  };
-  // Keys of step st present in the softmax: bit j for key st*32 + j (wave-uniform).
-  auto present = [&](int st) -> uint32_t {
-    const int base = st * STEP;
-    uint32_t bits = base + STEP <= len ? 0xffffffffu : (base < len ? (1u << (len - base)) - 1u : 0u);
-    if constexpr (PAGED) {
-#pragma unroll
-      for (int gi = 0; gi < 4; ++gi)
-        if (block_of(base + 8 * gi) >= (uint32_t)p.nb) bits &= ~(0xffu << (8 * gi));
-    }
-    return bits;
   };
 
   // V^T operand chunks (vt_operand): lane 4kk + q of group g reads keys K_g[kk] and
@@ -1711,15 +1720,13 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
   const int vt_key = 4 * g + ((lane & 15) >> 2);
   const int vt_col = 8 * (lane & 3);
 
-  float m = kNegInf, l = 0.f;  // query n's state; l sums the keys of this lane group
+  float m = kNegInf, l = 0.f;  // query n's state (m in units of scale * log2 e); l sums this lane group's keys
   f32x4 acc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // One step on the staged tile. FULL: all 32 keys present (every step of a row but its
-  // last, unless a block id is invalid), so the scores need no mask.
-  auto compute = [&](int buf, uint32_t bits, auto full_c) __attribute__((always_inline)) {
-    constexpr bool FULL = decltype(full_c)::value;
+  // One step on the staged tile; keys whose bit is clear score -inf.
+  auto compute = [&](int buf, uint32_t bits) __attribute__((always_inline)) {
     const char* lds_k = s_tile[buf];
     const char* lds_v = lds_k + STEP * kRowPad;
     // K operand of tile t, slab s: key 16t + n, dims 32s + 8g .. +8.
@@ -1737,21 +1744,32 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
 #pragma unroll
       for (int db = 0; db < 4; ++db) vt[db] = vt_operand(row_a, row_b, db);
     }
-    // Scores of keys 16t + 4g + i for query n.
+    // Raw scores of keys 16t + 4g + i for query n. The scale (positive) multiplies
+    // inside the exponent's FMA, so the maximum is taken on raw scores and scaled once.
     float sv[8];
-    float mx = kNegInf;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kk = 16 * t + 4 * g + i;
-        sv[4 * t + i] = sc[t][i] * p.scale_log2;
-        if constexpr (!FULL) sv[4 * t + i] = ((bits >> kk) & 1u) ? sv[4 * t + i] : kNegInf;
-        mx = fmaxf(mx, sv[4 * t + i]);
-      }
-    mx = fmaxf(mx, xor_lane<16>(mx));
-    mx = fmaxf(mx, xor_lane<32>(mx));
-    const float mn = fmaxf(m, mx);
+      for (int i = 0; i < 4; ++i) sv[4 * t + i] = sc[t][i];
+    if (bits != 0xffffffffu) {  // wave-uniform: a row's last step or an invalid block
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sv[4 * t + i] = ((bits >> (16 * t + 4 * g + i)) & 1u) ? sv[4 * t + i] : kNegInf;
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+    // Maximum over the 4 lane groups: a permlane swap of a register with itself leaves
+    // a lane's own value in one result and its partner's in the other.
+    {
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+    }
+    const float mn = fmaxf(m, mx * p.scale_log2);
     const float ref = mn == kNegInf ? 0.f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m - ref);
     // The accumulators are rescaled only when some query's maximum grew (alpha is
@@ -1764,8 +1782,8 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
     uint32_t pw[4], pr[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float p0 = __builtin_amdgcn_exp2f(sv[2 * k] - ref);
-      const float p1 = __builtin_amdgcn_exp2f(sv[2 * k + 1] - ref);
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(sv[2 * k], p.scale_log2, -ref));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(sv[2 * k + 1], p.scale_log2, -ref));
       const uint32_t w = pack2<DT>(p0, p1);
       pw[k] = w;
       if constexpr (DT == SKV_BF16) {
@@ -1788,44 +1806,61 @@ __global__ __launch_bounds__(64 * kWaves) void mqt_attention_kernel(AttnParams p
     }
   };
 
-  // A ring of kRing register slots: step st's loads live in slot st % kRing from their
-  // issue (kRing - 1 steps ahead) until they are staged into LDS buffer st % 2 during
-  // step st - 1. The loop is unrolled by kRing so every slot index is a constant, and
-  // loads are issued unconditionally (past the row's last step they are out of range
-  // and return zeros without a memory access), so the compiler's wait before staging a
-  // step counts only that step's loads and leaves the later ones in flight.
-  constexpr int kRing = 4;
-  const int nsteps = (len + STEP - 1) / STEP;
-  uint4 kr[kRing], vr[kRing];
-#pragma unroll
-  for (int i = 0; i < kRing; ++i) issue(i, kr[i], vr[i]);
+  // Step st's loads live in register slot st % 2 from their issue (one step ahead)
+  // until they are staged into LDS buffer st % 2 during step st - 1; its presence bits
+  // ride along in pbits. The loop is unrolled by 2 so the slot indices are constants,
+  // and loads are issued unconditionally (past the part's last step they are out of
+  // range and return zeros without a memory access), so the wait before staging a step
+  // counts only that step's loads. Both parts run the same number of steps, so every
+  // wave reaches every barrier.
+  uint4 kr[2], vr[2];
+  uint32_t pbits[2];
+  pbits[0] = issue(st0, kr[0], vr[0]);
+  pbits[1] = issue(st0 + 1, kr[1], vr[1]);
   stage(0, kr[0], vr[0]);
   lds_barrier();
   auto body = [&](int st, auto slot_c) __attribute__((always_inline)) {
-    constexpr int SLOT = decltype(slot_c)::value;  // st % kRing
-    constexpr int NEXT = (SLOT + 1) % kRing;
-    if (st + 1 < nsteps) stage((st + 1) & 1, kr[NEXT], vr[NEXT]);
-    issue(st + kRing, kr[SLOT], vr[SLOT]);
-    const uint32_t bits = present(st);
-    if (bits == 0xffffffffu)
-      compute(st & 1, bits, std::true_type{});
-    else
-      compute(st & 1, bits, std::false_type{});
+    constexpr int SLOT = decltype(slot_c)::value;  // st % 2
+    const uint32_t bits = pbits[SLOT];
+    if (st + 1 < nsteps) stage((st + 1) & 1, kr[SLOT ^ 1], vr[SLOT ^ 1]);
+    pbits[SLOT] = issue(st0 + st + 2, kr[SLOT], vr[SLOT]);
+    compute(st & 1, bits);
     lds_barrier();
   };
-  for (int st = 0; st < nsteps; st += kRing) {
+  for (int st = 0; st < nsteps; st += 2) {
     body(st, std::integral_constant<int, 0>{});
     if (st + 1 >= nsteps) break;
     body(st + 1, std::integral_constant<int, 1>{});
-    if (st + 2 >= nsteps) break;
-    body(st + 2, std::integral_constant<int, 2>{});
-    if (st + 3 >= nsteps) break;
-    body(st + 3, std::integral_constant<int, 3>{});
   }
   // Row sums over the 4 lane groups (the max is common to them).
   l += xor_lane<16>(l);
   l += xor_lane<32>(l);
-  if (!q_ok) return;
+  // Part 1 hands (max, sum, accumulators) to part 0 through LDS: 18 floats per lane, one
+  // block of 64 x 18 per query tile, in the tiles, which are free after the loop's last
+  // barrier.
+  float* xs = reinterpret_cast<float*>(&s_tiles[0][0][0]) + wave * (18 * 64);
+  static_assert(kWaves * 18 * 64 * sizeof(float) <= sizeof(s_tiles), "mqt_attention_kernel: merge area");
+  if (part == 1) {
+    xs[lane] = m;
+    xs[64 + lane] = l;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[128 + (4 * db + i) * 64 + lane] = acc[db][i];
+  }
+  lds_barrier();
+  if (part == 1 || !q_ok) return;
+  {
+    const float m1 = xs[lane], l1 = xs[64 + lane];
+    const float mm = fmaxf(m, m1);
+    const float ref = mm == kNegInf ? 0.f : mm;
+    const float a0 = __builtin_amdgcn_exp2f(m - ref), a1 = __builtin_amdgcn_exp2f(m1 - ref);
+    l = a0 * l + a1 * l1;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[db][i] = a0 * acc[db][i] + a1 * xs[128 + (4 * db + i) * 64 + lane];
+  }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   uint2* o = reinterpret_cast<uint2*>(p.o + (int64_t)b * p.osb + (int64_t)qi * p.osq + (int64_t)h * p.osh);
 #pragma unroll
@@ -2018,15 +2053,17 @@ template <bool PAGED>
 void launch_mqt(int32_t dtype, const AttnParams& p, hipStream_t s) {
   const dim3 grid((uint32_t)(p.heads * cdiv(p.qlen, kMqtQueries)), (uint32_t)p.batch, 1u);
   if (dtype == SKV_BF16)
-    hipLaunchKernelGGL((mqt_attention_kernel<SKV_BF16, PAGED>), grid, dim3(64 * kWaves), 0, s, p);
+    hipLaunchKernelGGL((mqt_attention_kernel<SKV_BF16, PAGED>), grid, dim3(64 * kWaves * kMqtParts), 0, s, p);
   else
-    hipLaunchKernelGGL((mqt_attention_kernel<SKV_F16, PAGED>), grid, dim3(64 * kWaves), 0, s, p);
+    hipLaunchKernelGGL((mqt_attention_kernel<SKV_F16, PAGED>), grid, dim3(64 * kWaves * kMqtParts), 0, s, p);
 }
 
-// Whether the 64-query kernel serves a multi-query launch: enough queries per row, and
-// enough (row, head, 64 queries) workgroups to fill the GPU without splitting keys.
+// Whether the 64-query kernel serves a multi-query launch: enough queries per row,
+// enough (row, head, 64 queries) workgroups to fill the GPU without splitting keys
+// across workgroups, and a positive scale (its maximum is taken on unscaled scores).
 bool use_mqt(const AttnParams& p) {
-  return p.qlen >= kMqtQueries && (int64_t)p.batch * p.heads * cdiv(p.qlen, kMqtQueries) >= device_cu_count() &&
+  return p.qlen >= kMqtQueries && p.scale_log2 > 0.f &&
+         (int64_t)p.batch * p.heads * cdiv(p.qlen, kMqtQueries) >= device_cu_count() &&
          (int64_t)p.heads * cdiv(p.qlen, kMqtQueries) <= 0x7fffffff;
 }
 

@@ -154,6 +154,20 @@ def test_many_queries_contiguous(cuda, dtype, qlen, rows):
     print(f"q_len {qlen} {dtype}: max err {err:.2e}")
 
 
+@pytest.mark.parametrize("scale", [-0.125, 0.0])
+def test_many_queries_non_positive_scale(cuda, scale):
+    """A scale of 0 or below at a 64-query-tile shape: the scores' maximum then is not the scaled maximum
+    of the raw scores, and the result still matches the oracle."""
+    dtype, h, qlen, rows = torch.bfloat16, 20, 64, 16
+    assert mqt_selected(rows, h, qlen)
+    lens = ([1500, 0, 1, 33, 700, 1499, 64, 95] * 2)[:rows]
+    slots = ([3, 0, 5, 1, 1, 2, 4, 0] * 2)[:rows]
+    g, q, lens_t, slots_t, layer = cross_case(cuda, dtype, qlen, 123, lens, slots, h=h)
+    out = native.dense_attention(q, g[:, layer, 0], g[:, layer, 1], lens_t, 1500, scale, slot_ids=slots_t)
+    want = O.dense_attention(f64(q), f64(g[:, layer, 0]), f64(g[:, layer, 1]), lens, scale, slot_ids=slots)
+    check(out, want, dtype, f"64-query tiles, scale {scale}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("kv_heads", [20, 4])
 def test_encoder_attention_shape_paged(cuda, dtype, kv_heads):
@@ -165,7 +179,8 @@ def test_encoder_attention_shape_paged(cuda, dtype, kv_heads):
     kp = torch.randn(nb, bs, kv_heads, 64, generator=gen).to(cuda, dtype)
     vp = torch.randn(nb, bs, kv_heads, 64, generator=gen).to(cuda, dtype)
     tables = torch.randperm(nb, generator=gen)[: 2 * maxblk].view(2, maxblk).to(torch.int32)
-    tables[1, 9] = -1
+    tables[1, 9] = -1          # keys 144..159: in the first half of the row's 32 steps
+    tables[1, 50] = nb + 7     # keys 800..815: in the second half
     rows, lens = [0, 1], [1500, 1001]
     assert mqt_selected(len(rows), h, qlen)
     q = torch.randn(len(rows), qlen, h, 64, generator=gen).to(cuda, dtype)
