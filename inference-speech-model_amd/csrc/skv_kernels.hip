@@ -1616,7 +1616,7 @@ mqt_attention_kernel(AttnParams p) {
   static_assert(kMqtParts == 2, "mqt_attention_kernel: the end-of-kernel merge is written for two parts");
   constexpr int D = 64;
   constexpr int STEP = 32;                       // keys per step, 8 per wave
-  constexpr int kRowPad = D * 2 + 16;            // LDS row of one key: 128 bytes + 16 of padding
+  constexpr int kRowPad = D * 2 + 32;            // LDS row of one key: 128 bytes + 32 of padding
   constexpr int kTileBytes = 2 * STEP * kRowPad; // K rows, then V rows
   __shared__ __attribute__((aligned(16))) char s_tiles[kMqtParts][2][kTileBytes];
 
@@ -1673,6 +1673,16 @@ mqt_attention_kernel(AttnParams p) {
   const __amdgpu_buffer_rsrc_t vres =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(vb), (short)0, (int)p.kv_bytes, kBufWord3);
 
+  // Whether every block id under [0, len) is a pool block (the normal case): one vector
+  // read of the table row; the steps' presence bits then depend on len only.
+  bool row_ok = true;
+  if constexpr (PAGED) {
+    const int nblk = (len + p.bs - 1) >> p.bs_shift;
+    bool bad = false;
+    for (int e = lane; e < nblk; e += 64) bad |= trow[e] >= (uint32_t)p.nb;
+    row_ok = __builtin_amdgcn_ballot_w64(bad) == 0;
+  }
+
   // This part's steps: [st0, st0 + nsteps) of the row's ceil(len / 32), keys below lim.
   const int nsteps = ((len + STEP - 1) / STEP + kMqtParts - 1) / kMqtParts;
   const int st0 = part * nsteps;
@@ -1681,9 +1691,10 @@ mqt_attention_kernel(AttnParams p) {
   // Issues step st's loads for this wave (keys st*32 + 8*wave + (lane >> 3), byte column
   // 16 * (lane & 7); at or past lim, or behind an invalid block, the offset is out of
   // range and the load returns zeros without a memory access) and returns the step's
-  // presence bits: bit j for key st*32 + j in the softmax (wave-uniform). The step's
-  // block ids (one per 8 keys, block size >= 8, clamped to the row's last key so the
-  // index stays inside the row) are read in one batch of scalar loads.
+  // presence bits: bit j for key st*32 + j in the softmax (wave-uniform). Block ids are
+  // read with scalar loads (one per 8 keys, block size >= 8, clamped to the row's last
+  // key so the index stays inside the row): the wave's own, and on a row with an
+  // invalid id the step's four, in one batch.
   const int nat_row = lane >> 3, nat_col = (lane & 7) * 16;
   auto issue = [&](int st, uint4& kr, uint4& vr) -> uint32_t {
     const int base = st * STEP;
@@ -1691,13 +1702,15 @@ mqt_attention_kernel(AttnParams p) {
     uint32_t bits = base + STEP <= len ? 0xffffffffu : (base < len ? (1u << (len - base)) - 1u : 0u);
     uint32_t off;
     if constexpr (PAGED) {
-      uint32_t blk[4];
+      if (!row_ok) {
+        uint32_t blk[4];
 #pragma unroll
-      for (int gi = 0; gi < 4; ++gi) blk[gi] = trow[(uint32_t)min(base + 8 * gi, len - 1) >> p.bs_shift];
+        for (int gi = 0; gi < 4; ++gi) blk[gi] = trow[(uint32_t)min(base + 8 * gi, len - 1) >> p.bs_shift];
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi)
+          if (blk[gi] >= (uint32_t)p.nb) bits &= ~(0xffu << (8 * gi));
+      }
       const uint32_t own = trow[(uint32_t)min(base + 8 * wave, len - 1) >> p.bs_shift];
-#pragma unroll
-      for (int gi = 0; gi < 4; ++gi)
-        if (blk[gi] >= (uint32_t)p.nb) bits &= ~(0xffu << (8 * gi));
       off = key < lim && own < (uint32_t)p.nb
                 ? (own * (uint32_t)p.bs + ((uint32_t)key & ((uint32_t)p.bs - 1u))) * row_bytes + col_base +
                       (uint32_t)nat_col
@@ -1724,6 +1737,12 @@ mqt_attention_kernel(AttnParams p) {
   f32x4 acc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // fp16 sums P on the matrix cores: a product with an operand of ones gives every lane
+  // its query's sum over the step's 32 keys (the rounded weights, as the PV product
+  // uses them). bf16 sums the unrounded weights on the VALU: its P is two operands.
+  constexpr bool kOnesSum = DT == SKV_F16;
+  f32x4 l4 = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint4 ones = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
 
   // One step on the staged tile; keys whose bit is clear score -inf.
   auto compute = [&](int buf, uint32_t bits) __attribute__((always_inline)) {
@@ -1776,7 +1795,10 @@ mqt_attention_kernel(AttnParams p) {
     // exactly 1 for the others): past the first steps most steps skip it.
     const bool rescale = __builtin_amdgcn_ballot_w64(mn != m) != 0;
     m = mn;
-    l *= alpha;
+    if constexpr (kOnesSum)
+      l4 *= alpha;
+    else
+      l *= alpha;
     // P^T operand, as in mq_attention_kernel: fp16 rounds P once and sums the rounded
     // values; bf16 adds the product of the rounded remainder.
     uint32_t pw[4], pr[4];
@@ -1789,8 +1811,6 @@ mqt_attention_kernel(AttnParams p) {
       if constexpr (DT == SKV_BF16) {
         pr[k] = pack2<DT>(p0 - lo16<DT>(w), p1 - hi16<DT>(w));
         l += p0 + p1;
-      } else {
-        l += lo16<DT>(w) + hi16<DT>(w);
       }
     }
     const uint4 pt = make_uint4(pw[0], pw[1], pw[2], pw[3]);
@@ -1804,6 +1824,7 @@ mqt_attention_kernel(AttnParams p) {
       acc[db] = mfma_16x16x32<DT>(vt[db], pt, acc[db]);
       if constexpr (DT == SKV_BF16) acc[db] = mfma_16x16x32<DT>(vt[db], prt, acc[db]);
     }
+    if constexpr (kOnesSum) l4 = mfma_16x16x32<DT>(ones, pt, l4);
   };
 
   // Step st's loads live in register slot st % 2 from their issue (one step ahead)
@@ -1832,9 +1853,12 @@ mqt_attention_kernel(AttnParams p) {
     if (st + 1 >= nsteps) break;
     body(st + 1, std::integral_constant<int, 1>{});
   }
-  // Row sums over the 4 lane groups (the max is common to them).
-  l += xor_lane<16>(l);
-  l += xor_lane<32>(l);
+  if constexpr (kOnesSum) {
+    l = l4[0];
+  } else {  // row sums over the 4 lane groups (the max is common to them)
+    l += xor_lane<16>(l);
+    l += xor_lane<32>(l);
+  }
   // Part 1 hands (max, sum, accumulators) to part 0 through LDS: 18 floats per lane, one
   // block of 64 x 18 per query tile, in the tiles, which are free after the loop's last
   // barrier.
