@@ -19,6 +19,8 @@ x 64, batch 64):
                             gather kernels
   large_v3_prefill_cross_attention  the prompt prefill's cross-attention, 128 requests x q_len
                             1 / 4 / 16 (multi-query matrix-core kernel for q_len >= 2)
+  large_v3_encoder_attention  encoder attention over paged blocks (1500 queries, 64-query tiles)
+  large_v3_argmax           greedy tokens of a decode step (64 x 51866 logits) with slot feedback
   tts_decode                the streaming multi-codebook TTS engine (reference TTS
                             model's default shape, 64 requests x 256 frames)
   config1_decode            the Whisper-tiny-shaped decoder of config 1 (4 requests x 64 greedy
@@ -448,6 +450,31 @@ def large_v3_append_gather(torch, native, dev, a):
     return out
 
 
+def large_v3_argmax(torch, native, dev, a):
+    """Greedy token selection of a large-v3 decode step: the first maximum of each of 64 rows of
+    51866 bf16 logits (the LM head's output, which the decode reads right after writing it, so it
+    is timed cache-resident), with the slot feedback the graph decode uses (next-step tokens, EOS
+    flags and count). Bytes: the logits read plus the token outputs."""
+    rows, vocab = 64, 51866
+    g = torch.Generator(device=dev).manual_seed(a.seed + 600)
+    logits = torch.randn(rows, vocab, generator=g, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(rows, dtype=torch.int64, device=dev)
+    row_slots = torch.arange(rows, dtype=torch.int32, device=dev)
+    slot_tokens = torch.zeros(rows, dtype=torch.int64, device=dev)
+    slot_eos = torch.full((rows,), 50257, dtype=torch.int64, device=dev)
+    slot_finished = torch.zeros(rows, dtype=torch.int32, device=dev)
+    finished = torch.zeros(1, dtype=torch.int64, device=dev)
+    fns = [lambda: native.argmax(logits, out=out, row_slots=row_slots, slot_tokens=slot_tokens, slot_eos=slot_eos,
+                                 slot_finished=slot_finished, finished_count=finished)]
+    us = graph_launch_us(torch, fns, per_fn=8, replays=5)
+    if not torch.equal(out, torch.argmax(logits.float(), dim=-1)):
+        raise RuntimeError("large_v3_argmax: tokens differ from torch.argmax")
+    byts = rows * vocab * 2 + rows * 8 * 2
+    return {"shape": "bf16, 64 rows x 51866 logits, slot feedback (tokens, EOS flags and count)",
+            "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": byts,
+            "achieved_GBps": round(byts / (us * 1e-6) / 1e9, 1), "frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def large_v3_decode(torch, dev, a):
     """Greedy decode of decode_batch requests x decode_tokens tokens through the scheduler's graphs."""
     from speech_serving import (BlockManager, DualCacheManager, EncoderBlockManager, MemoryGuard,
@@ -779,6 +806,7 @@ def main():
         legs.update(large_v3_append_gather(torch, native, dev, a))
         legs["large_v3_prefill_cross_attention"] = large_v3_prefill_cross(torch, native, dev, a)
         legs["large_v3_encoder_attention"] = large_v3_encoder_attention(torch, native, dev, a)
+        legs["large_v3_argmax"] = large_v3_argmax(torch, native, dev, a)
 
     sets = paged_sets(torch, native, dev, dtype, a.batch, a.heads, a.head_dim, a.block_size, a.pool_blocks,
                       a.max_ctx, a.seed, a.chunk)

@@ -267,13 +267,16 @@ __global__ __launch_bounds__(256) void cross_copy_kernel(CrossCopyParams p) {
 // slot s = row_slots[r] is in [0, num_slots): slot_tokens[s] = token (the next
 // step's input), and when the token is the slot's EOS id (slot_eos[s] >= 0) and
 // the slot is not yet finished, slot_finished[s] = 1 and finished_count += 1.
-// One 1024-thread workgroup per row reads the row as 32-bit words through a
-// buffer descriptor (past-the-end words read as zero and are not compared),
-// kArgmaxWords words per thread in flight; a 16-bit row that starts in the
-// middle of a word has its first element handled alone.
+// One workgroup per row reads the row as 16-byte vectors of 32-bit words through a
+// buffer descriptor (reads past the row's last word return zeros and are not
+// compared), kArgmaxVecs vectors per thread in flight. A thread visits its elements
+// in increasing index order and keeps the first strictly greater value, so each
+// element costs a compare and two selects; a NaN only sets a flag, and a thread that
+// saw one rescans its elements for the first NaN (NaN counts as the maximum). A
+// 16-bit row that starts in the middle of a word has its first element handled alone.
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxThreads = 1024;
-constexpr int kArgmaxWords = 32;  // words per thread per pass: 65536 16-bit logits in one pass
+constexpr int kArgmaxVecs = 4;  // 16-byte vectors per thread per pass: 32768 16-bit logits
 
 __device__ __forceinline__ bool argmax_better(float v1, int i1, float v2, int i2) {
   const bool n1 = v1 != v1, n2 = v2 != v2;
@@ -287,6 +290,13 @@ template <> __device__ __forceinline__ float half_word<SKV_F16>(uint32_t w, int 
 }
 template <> __device__ __forceinline__ float half_word<SKV_BF16>(uint32_t w, int hi) {
   return __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
+}
+template <int DT> __device__ __forceinline__ float word_elt(uint32_t w, int e) {
+  if constexpr (DT == SKV_F32) {
+    return __uint_as_float(w);
+  } else {
+    return half_word<DT>(w, e);
+  }
 }
 
 struct SlotFeedback {
@@ -302,18 +312,11 @@ template <int DT>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __restrict__ logits, int64_t row_bytes,
                                                                 int32_t vocab, int64_t* __restrict__ out,
                                                                 SlotFeedback f) {
-  __shared__ float s_v[kArgmaxThreads / 64];
-  __shared__ int s_i[kArgmaxThreads / 64];
+  constexpr int kAmWaves = kArgmaxThreads / 64;
+  __shared__ float s_v[kAmWaves];
+  __shared__ int s_i[kAmWaves];
   const int r = blockIdx.x;
   const char* row = logits + (int64_t)r * row_bytes;
-  float best = kNegInf;
-  int bi = 0x7fffffff;
-  auto consider = [&](float v, int i) {
-    if (argmax_better(v, i, best, bi)) {
-      best = v;
-      bi = i;
-    }
-  };
   // Elements per word, the element held alone before the first word, and the word count.
   constexpr int EPW = DT == SKV_F32 ? 1 : 2;
   const int head = (EPW == 2 && ((uintptr_t)row & 3u)) ? 1 : 0;
@@ -321,24 +324,62 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
   const int nw = (vocab - head) / EPW;
   const __amdgpu_buffer_rsrc_t res =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(words), (short)0, nw * 4, kBufWord3);
-  for (int w0 = threadIdx.x; w0 < nw; w0 += kArgmaxThreads * kArgmaxWords) {
-    uint32_t x[kArgmaxWords];
+  // The candidate starts at the thread's first element (value -inf), so a row whose maximum is
+  // -inf resolves to its first index like the others.
+  float best = kNegInf;
+  int bi = 4 * (int)threadIdx.x < nw ? head + EPW * 4 * (int)threadIdx.x : 0x7fffffff;
+  bool nan_seen = false;
+  // Thread t's vectors: words 4 * (t + kArgmaxThreads * k) .. +3, k = 0, 1, ...
+  constexpr int kPassWords = 4 * kArgmaxThreads * kArgmaxVecs;
+  for (int p0 = 0; p0 < nw; p0 += kPassWords) {
+    u32x4 x[kArgmaxVecs];
 #pragma unroll
-    for (int k = 0; k < kArgmaxWords; ++k)
-      x[k] = __builtin_amdgcn_raw_buffer_load_b32(res, (uint32_t)(w0 + k * kArgmaxThreads) * 4u, 0, kBufNt);
+    for (int k = 0; k < kArgmaxVecs; ++k)
+      x[k] = __builtin_amdgcn_raw_buffer_load_b128(
+          res, (uint32_t)(p0 + 4 * ((int)threadIdx.x + kArgmaxThreads * k)) * 4u, 0, kBufNt);
 #pragma unroll
-    for (int k = 0; k < kArgmaxWords; ++k) {
-      const int w = w0 + k * kArgmaxThreads;
-      if (w < nw) {
-        if constexpr (EPW == 1) {
-          consider(__uint_as_float(x[k]), w);
-        } else {
-          consider(half_word<DT>(x[k], 0), head + 2 * w);
-          consider(half_word<DT>(x[k], 1), head + 2 * w + 1);
+    for (int k = 0; k < kArgmaxVecs; ++k) {
+      const int w0 = p0 + 4 * ((int)threadIdx.x + kArgmaxThreads * k);
+      const int valid = min(max(nw - w0, 0), 4);  // words of this vector inside the row
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int e = 0; e < EPW; ++e) {
+          float v = word_elt<DT>(x[k][j], e);
+          v = j < valid ? v : kNegInf;
+          const int i = head + EPW * (w0 + j) + e;
+          const bool gt = v > best;
+          best = gt ? v : best;
+          bi = gt ? i : bi;
+          nan_seen |= v != v;
         }
       }
     }
   }
+  if (nan_seen) {  // rare: the first NaN among this thread's elements wins
+    int ni = 0x7fffffff;
+    for (int p0 = 0; p0 < nw; p0 += kPassWords)
+      for (int k = 0; k < kArgmaxVecs; ++k) {
+        const int w0 = p0 + 4 * ((int)threadIdx.x + kArgmaxThreads * k);
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(res, (uint32_t)w0 * 4u, 0, kBufNt);
+        for (int j = 0; j < 4; ++j)
+          for (int e = 0; e < EPW; ++e) {
+            const float v = word_elt<DT>(x[j], e);
+            const int i = head + EPW * (w0 + j) + e;
+            if (w0 + j < nw && v != v && i < ni) ni = i;
+          }
+      }
+    if (ni != 0x7fffffff) {
+      best = __builtin_nanf("");
+      bi = ni;
+    }
+  }
+  auto consider = [&](float v, int i) {
+    if (argmax_better(v, i, best, bi)) {
+      best = v;
+      bi = i;
+    }
+  };
   if constexpr (EPW == 2) {
     if (threadIdx.x == 0) {
       const uint16_t* e = reinterpret_cast<const uint16_t*>(row);
@@ -358,8 +399,17 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
     s_i[wave] = bi;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kArgmaxThreads / 64; ++w) consider(s_v[w], s_i[w]);
+  if (wave != 0) return;
+  const int lane = threadIdx.x;
+  best = lane < kAmWaves ? s_v[lane] : kNegInf;
+  bi = lane < kAmWaves ? s_i[lane] : 0x7fffffff;
+#pragma unroll
+  for (int off = kAmWaves / 2; off >= 1; off >>= 1) {
+    const float v2 = __shfl_xor(best, off, 64);
+    const int i2 = __shfl_xor(bi, off, 64);
+    consider(v2, i2);
+  }
+  if (lane == 0) {
     const int64_t tok = bi == 0x7fffffff ? 0 : bi;
     out[r] = tok;
     if (f.row_slots) {
