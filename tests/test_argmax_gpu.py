@@ -34,6 +34,32 @@ def test_argmax_matches_numpy_first_max(cuda, dtype, vocab):
         assert got[1] == 5 and got[2] == 0 and got[3] == vocab // 2 and got[4] == 3
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_argmax_row_edges(cuda, dtype):
+    """Rows that start 2 bytes into a word (a lone first element), an odd element count (a lone last
+    element), NaNs in those lone elements and in two threads' ranges, and rows whose maximum is -inf."""
+    gen = torch.Generator().manual_seed(11)
+    vocab = 40001
+    full = torch.randn(8, vocab + 1, generator=gen).to(dtype)
+    x = full[:, 1:]                       # 16-bit rows start 2 bytes into a word
+    x[0, :] = -float("inf")               # maximum -inf: index 0
+    x[1, 0] = float("nan")                # NaN in the lone first element
+    x[2, vocab - 1] = float("nan")        # NaN in the lone last element
+    x[3, 30000] = float("nan")            # NaNs in two threads' ranges: the first wins
+    x[3, 9000] = float("nan")
+    x[4, :] = -float("inf")
+    x[4, vocab - 1] = 0.0                 # the maximum in the lone last element
+    x[5, :] = 2.0                         # all equal: index 0
+    got = native.argmax(x.to(cuda)).cpu().tolist()
+    xf = x.float().numpy()
+    want = []
+    for r in range(x.shape[0]):
+        nan = np.flatnonzero(np.isnan(xf[r]))
+        want.append(int(nan[0]) if nan.size else int(np.argmax(xf[r])))
+    assert got == want
+    assert got[:6] == [0, 0, vocab - 1, 9000, vocab - 1, 0]
+
+
 def test_argmax_strided_rows_and_slot_feedback(cuda):
     gen = torch.Generator().manual_seed(0)
     full = torch.randn(5, 1, 300, generator=gen).to(cuda, torch.bfloat16)
