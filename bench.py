@@ -21,6 +21,7 @@ x 64, batch 64):
                             1 / 4 / 16 (multi-query matrix-core kernel for q_len >= 2)
   large_v3_encoder_attention  encoder attention over paged blocks (1500 queries, 64-query tiles)
   large_v3_argmax           greedy tokens of a decode step (64 x 51866 logits) with slot feedback
+  large_v3_cross_copy       one request's encoder K/V (32 layers) into its decode slot
   tts_decode                the streaming multi-codebook TTS engine (reference TTS
                             model's default shape, 64 requests x 256 frames)
   config1_decode            the Whisper-tiny-shaped decoder of config 1 (4 requests x 64 greedy
@@ -81,11 +82,13 @@ def parse():
     ap.add_argument("--decode-tokens", type=int, default=448)
     ap.add_argument("--decode-layers", type=int, default=32)
     ap.add_argument("--no-serving", action="store_true", help="skip the large-v3 256-request serving burst")
-    ap.add_argument("--mode", choices=["attention", "copy", "decode", "serving", "tts", "config1", "prefill"],
+    ap.add_argument("--mode", choices=["attention", "copy", "decode", "serving", "tts", "config1", "prefill",
+                                       "copies"],
                     default="attention",
                     help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling; "
                          "decode: only the large-v3-shaped greedy decode; serving: only the large-v3 serving "
-                         "burst; tts: only the streaming TTS engine")
+                         "burst; tts: only the streaming TTS engine; copies: only the large-v3 append, gather, "
+                         "slot handoff copy and argmax")
     ap.add_argument("--copy-mib", type=int, default=512)
     return ap.parse_args()
 
@@ -450,6 +453,31 @@ def large_v3_append_gather(torch, native, dev, a):
     return out
 
 
+def large_v3_cross_copy(torch, native, dev, a):
+    """Encoder K/V into a decode slot (the graph decode's slot handoff) at the large-v3 shape: one request's
+    32 layers of K and V, 20 heads x 1500 positions x 64 bf16 each, into the slot's region of the
+    slot-major cross-attention buffer, one launch. Two rotating request/slot pairs (2 x 492 MB moved >
+    the 256 MB last-level cache). Bytes: every element read once and written once."""
+    L, h, t, d, dt = 32, 20, 1500, 64, torch.bfloat16
+    pairs = []
+    for i in range(2):
+        g = torch.Generator(device=dev).manual_seed(a.seed + 700 + i)
+        ks = [torch.randn(h, t, d, generator=g, device=dev, dtype=dt) for _ in range(L)]
+        vs = [torch.randn(h, t, d, generator=g, device=dev, dtype=dt) for _ in range(L)]
+        pairs.append((ks, vs, torch.empty(L, 2, h, t, d, device=dev, dtype=dt)))
+    fns = [lambda pr=pr: native.copy_cross_kv(pr[0], pr[1], pr[2], t) for pr in pairs]
+    us = graph_launch_us(torch, fns, per_fn=4, replays=5)
+    ks, vs, dst = pairs[0]
+    if not (torch.equal(dst[0, 0], ks[0]) and torch.equal(dst[L - 1, 1], vs[L - 1])):
+        raise RuntimeError("large_v3_cross_copy: slot contents differ from the sources")
+    byts = 2 * L * 2 * h * t * d * 2
+    del pairs, fns, ks, vs, dst
+    torch.cuda.empty_cache()
+    return {"shape": "bf16, one request's 32 layers x (K, V) x 20 heads x 1500 positions x 64 into its decode slot",
+            "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": byts,
+            "achieved_GBps": round(byts / (us * 1e-6) / 1e9, 1), "frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def large_v3_argmax(torch, native, dev, a):
     """Greedy token selection of a large-v3 decode step: the first maximum of each of 64 rows of
     51866 bf16 logits (the LM head's output, which the decode reads right after writing it, so it
@@ -790,6 +818,13 @@ def main():
         print(json.dumps({"large_v3_prefill_cross_attention": large_v3_prefill_cross(torch, native, dev, a),
                           "large_v3_encoder_attention": large_v3_encoder_attention(torch, native, dev, a)}))
         return
+    if a.mode == "copies":  # the large-v3 append, gather, slot handoff copy and argmax alone
+        native.lib()
+        res = large_v3_append_gather(torch, native, dev, a)
+        res["large_v3_cross_copy"] = large_v3_cross_copy(torch, native, dev, a)
+        res["large_v3_argmax"] = large_v3_argmax(torch, native, dev, a)
+        print(json.dumps(res))
+        return
     if a.mode == "config1":  # the Whisper-tiny config-1 decode alone
         native.lib()
         print(json.dumps({"config1_decode": config1_decode(torch, dev, a)}))
@@ -807,6 +842,7 @@ def main():
         legs["large_v3_prefill_cross_attention"] = large_v3_prefill_cross(torch, native, dev, a)
         legs["large_v3_encoder_attention"] = large_v3_encoder_attention(torch, native, dev, a)
         legs["large_v3_argmax"] = large_v3_argmax(torch, native, dev, a)
+        legs["large_v3_cross_copy"] = large_v3_cross_copy(torch, native, dev, a)
 
     sets = paged_sets(torch, native, dev, dtype, a.batch, a.heads, a.head_dim, a.block_size, a.pool_blocks,
                       a.max_ctx, a.seed, a.chunk)
