@@ -1656,7 +1656,7 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
 // parts of 4 waves: part 0 takes the first half of the steps, part 1 the second,
 // each wave keeping its 16 queries' softmax state over its part's keys, and part 1
 // hands its state to part 0 through LDS at the end. The split puts 4 waves on each
-// SIMD (a 100-VGPR budget) where one part alone would leave 2: the per-step chain
+// SIMD (at most 128 VGPRs each) where one part alone would leave 2: the per-step chain
 // (products, softmax, products) is latency-bound, not issue-bound. Each wave runs
 // the same products as mq_attention_kernel on the shared step. Steps are
 // double-buffered in LDS with one barrier per step that orders LDS only; every
