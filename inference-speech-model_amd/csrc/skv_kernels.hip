@@ -1651,18 +1651,19 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
 // Multi-query attention with many queries per row (encoder attention over a
 // table of encoder blocks, q_len = T; long prompts), fp16/bf16, head_dim 64,
 // non-causal: one workgroup owns 64 queries of one (row, head), 16 per wave, and
-// walks the row's keys in 32-key steps staged in LDS, so K/V are read once per
+// walks the row's keys in 64-key steps staged in LDS, so K/V are read once per
 // 64 queries (mq_attention_kernel reads them once per 16). The workgroup is two
 // parts of 4 waves: part 0 takes the first half of the steps, part 1 the second,
 // each wave keeping its 16 queries' softmax state over its part's keys, and part 1
 // hands its state to part 0 through LDS at the end. The split puts 4 waves on each
 // SIMD (at most 128 VGPRs each) where one part alone would leave 2: the per-step chain
 // (products, softmax, products) is latency-bound, not issue-bound. Each wave runs
-// the same products as mq_attention_kernel on the shared step. Steps are
-// double-buffered in LDS with one barrier per step that orders LDS only; every
-// wave keeps the next step's global loads in flight (8 key rows of K and of V, 8
-// lanes per 128-byte row) and reads that step's block ids in one batch of scalar
-// loads when it issues them.
+// the same products as mq_attention_kernel on each 32-key half of the shared step
+// (the second half's score products do not wait for the first half's softmax).
+// Steps are double-buffered in LDS (80 KB per workgroup) with one barrier per step
+// that orders LDS only; every wave keeps the next step's global loads in flight (16
+// key rows of K and of V, 8 lanes per 128-byte row) and reads their block ids with
+// scalar loads when it issues them.
 // ---------------------------------------------------------------------------
 constexpr int kMqtQueries = 64;  // queries per workgroup, 16 per wave of a part
 constexpr int kMqtParts = 2;     // key halves per workgroup
@@ -1673,9 +1674,10 @@ mqt_attention_kernel(AttnParams p) {
   static_assert(kWaves * kMqQueries == kMqtQueries, "mqt_attention_kernel: 16 queries per wave");
   static_assert(kMqtParts == 2, "mqt_attention_kernel: the end-of-kernel merge is written for two parts");
   constexpr int D = 64;
-  constexpr int STEP = 32;                       // keys per step, 8 per wave
+  constexpr int STEP = 32;                       // keys per compute half-step
+  constexpr int LSTEP = 64;                      // keys per staged step, 16 per wave
   constexpr int kRowPad = D * 2 + 32;            // LDS row of one key: 128 bytes + 32 of padding
-  constexpr int kTileBytes = 2 * STEP * kRowPad; // K rows, then V rows
+  constexpr int kTileBytes = 2 * LSTEP * kRowPad; // K rows, then V rows
   __shared__ __attribute__((aligned(16))) char s_tiles[kMqtParts][2][kTileBytes];
 
   const int lane = threadIdx.x & 63;
@@ -1741,49 +1743,59 @@ mqt_attention_kernel(AttnParams p) {
     row_ok = __builtin_amdgcn_ballot_w64(bad) == 0;
   }
 
-  // This part's steps: [st0, st0 + nsteps) of the row's ceil(len / 32), keys below lim.
-  const int nsteps = ((len + STEP - 1) / STEP + kMqtParts - 1) / kMqtParts;
+  // This part's steps: [st0, st0 + nsteps) of the row's ceil(len / 64), keys below lim.
+  const int nsteps = ((len + LSTEP - 1) / LSTEP + kMqtParts - 1) / kMqtParts;
   const int st0 = part * nsteps;
-  const int lim = min(len, (st0 + nsteps) * STEP);
+  const int lim = min(len, (st0 + nsteps) * LSTEP);
 
-  // Issues step st's loads for this wave (keys st*32 + 8*wave + (lane >> 3), byte column
-  // 16 * (lane & 7); at or past lim, or behind an invalid block, the offset is out of
-  // range and the load returns zeros without a memory access) and returns the step's
-  // presence bits: bit j for key st*32 + j in the softmax (wave-uniform). Block ids are
-  // read with scalar loads (one per 8 keys, block size >= 8, clamped to the row's last
-  // key so the index stays inside the row): the wave's own, and on a row with an
-  // invalid id the step's four, in one batch.
+  // Issues step st's loads for this wave (keys st*64 + 16*wave + 8r + (lane >> 3) for
+  // r = 0, 1, byte column 16 * (lane & 7); at or past lim, or behind an invalid block,
+  // the offset is out of range and the load returns zeros without a memory access) and
+  // returns the step's presence bits: bit j for key st*64 + j in the softmax
+  // (wave-uniform). Block ids are read with scalar loads (one per 8 keys, block size
+  // >= 8, clamped to the row's last key so the index stays inside the row): the
+  // wave's own two, and on a row with an invalid id the step's eight, in one batch.
   const int nat_row = lane >> 3, nat_col = (lane & 7) * 16;
-  auto issue = [&](int st, uint4& kr, uint4& vr) -> uint32_t {
-    const int base = st * STEP;
-    const int key = base + 8 * wave + nat_row;
-    uint32_t bits = base + STEP <= len ? 0xffffffffu : (base < len ? (1u << (len - base)) - 1u : 0u);
-    uint32_t off;
+  auto issue = [&](int st, uint4 (&kr)[2], uint4 (&vr)[2]) -> uint64_t {
+    const int base = st * LSTEP;
+    uint64_t bits = base + LSTEP <= len ? ~0ull : (base < len ? (1ull << (len - base)) - 1ull : 0ull);
     if constexpr (PAGED) {
       if (!row_ok) {
-        uint32_t blk[4];
+        uint32_t blk[8];
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi) blk[gi] = trow[(uint32_t)min(base + 8 * gi, len - 1) >> p.bs_shift];
+        for (int gi = 0; gi < 8; ++gi) blk[gi] = trow[(uint32_t)min(base + 8 * gi, len - 1) >> p.bs_shift];
 #pragma unroll
-        for (int gi = 0; gi < 4; ++gi)
-          if (blk[gi] >= (uint32_t)p.nb) bits &= ~(0xffu << (8 * gi));
+        for (int gi = 0; gi < 8; ++gi)
+          if (blk[gi] >= (uint32_t)p.nb) bits &= ~(0xffull << (8 * gi));
       }
-      const uint32_t own = trow[(uint32_t)min(base + 8 * wave, len - 1) >> p.bs_shift];
-      off = key < lim && own < (uint32_t)p.nb
-                ? (own * (uint32_t)p.bs + ((uint32_t)key & ((uint32_t)p.bs - 1u))) * row_bytes + col_base +
-                      (uint32_t)nat_col
-                : kBufOutOfRange;
-    } else {
-      off = key < lim ? (uint32_t)key * row_bytes + (uint32_t)nat_col : kBufOutOfRange;
     }
-    kr = load_buf(kres, off);
-    vr = load_buf(vres, off);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int key0 = base + 16 * wave + 8 * r;
+      const int key = key0 + nat_row;
+      uint32_t off;
+      if constexpr (PAGED) {
+        const uint32_t own = trow[(uint32_t)min(key0, len - 1) >> p.bs_shift];
+        off = key < lim && own < (uint32_t)p.nb
+                  ? (own * (uint32_t)p.bs + ((uint32_t)key & ((uint32_t)p.bs - 1u))) * row_bytes + col_base +
+                        (uint32_t)nat_col
+                  : kBufOutOfRange;
+      } else {
+        off = key < lim ? (uint32_t)key * row_bytes + (uint32_t)nat_col : kBufOutOfRange;
+      }
+      kr[r] = load_buf(kres, off);
+      vr[r] = load_buf(vres, off);
+    }
     return bits;
   };
-  auto stage = [&](int buf, const uint4& kr, const uint4& vr) {
+  auto stage = [&](int buf, const uint4 (&kr)[2], const uint4 (&vr)[2]) {
     char* t = s_tile[buf];
-    *reinterpret_cast<uint4*>(t + (8 * wave + nat_row) * kRowPad + nat_col) = kr;
-    *reinterpret_cast<uint4*>(t + STEP * kRowPad + (8 * wave + nat_row) * kRowPad + nat_col) = vr;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = 16 * wave + 8 * r + nat_row;
+      *reinterpret_cast<uint4*>(t + row * kRowPad + nat_col) = kr[r];
+      *reinterpret_cast<uint4*>(t + LSTEP * kRowPad + row * kRowPad + nat_col) = vr[r];
+    }
   };
 
   // V^T operand chunks (vt_operand): lane 4kk + q of group g reads keys K_g[kk] and
@@ -1802,10 +1814,10 @@ mqt_attention_kernel(AttnParams p) {
   f32x4 l4 = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint4 ones = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
 
-  // One step on the staged tile; keys whose bit is clear score -inf.
-  auto compute = [&](int buf, uint32_t bits) __attribute__((always_inline)) {
-    const char* lds_k = s_tile[buf];
-    const char* lds_v = lds_k + STEP * kRowPad;
+  // One 32-key half of the staged step; keys whose bit is clear score -inf.
+  auto compute = [&](int buf, int half, uint32_t bits) __attribute__((always_inline)) {
+    const char* lds_k = s_tile[buf] + half * STEP * kRowPad;
+    const char* lds_v = s_tile[buf] + LSTEP * kRowPad + half * STEP * kRowPad;
     // K operand of tile t, slab s: key 16t + n, dims 32s + 8g .. +8.
     f32x4 sc[2];
 #pragma unroll
@@ -1892,18 +1904,19 @@ mqt_attention_kernel(AttnParams p) {
   // range and return zeros without a memory access), so the wait before staging a step
   // counts only that step's loads. Both parts run the same number of steps, so every
   // wave reaches every barrier.
-  uint4 kr[2], vr[2];
-  uint32_t pbits[2];
+  uint4 kr[2][2], vr[2][2];
+  uint64_t pbits[2];
   pbits[0] = issue(st0, kr[0], vr[0]);
   pbits[1] = issue(st0 + 1, kr[1], vr[1]);
   stage(0, kr[0], vr[0]);
   lds_barrier();
   auto body = [&](int st, auto slot_c) __attribute__((always_inline)) {
     constexpr int SLOT = decltype(slot_c)::value;  // st % 2
-    const uint32_t bits = pbits[SLOT];
+    const uint64_t bits = pbits[SLOT];
     if (st + 1 < nsteps) stage((st + 1) & 1, kr[SLOT ^ 1], vr[SLOT ^ 1]);
     pbits[SLOT] = issue(st0 + st + 2, kr[SLOT], vr[SLOT]);
-    compute(st & 1, bits);
+    compute(st & 1, 0, (uint32_t)bits);
+    if ((uint32_t)(bits >> 32) != 0u) compute(st & 1, 1, (uint32_t)(bits >> 32));  // a half with no key changes nothing
     lds_barrier();
   };
   for (int st = 0; st < nsteps; st += 2) {
