@@ -47,10 +47,11 @@ def run_case(cuda, dtype, bsz, qlen, h, hkv, d, bs, nb, ctx, causal, seed, chunk
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-def test_fused_decode_append(cuda, dtype):
-    out, want, _ = run_case(cuda, dtype, 16, 1, 8, 8, 64, 16, 512, [1, 2, 15, 16, 17, 100, 255, 256, 257, 300,
+@pytest.mark.parametrize("bs", [16, 32, 64])
+def test_fused_decode_append(cuda, dtype, bs):
+    out, want, _ = run_case(cuda, dtype, 16, 1, 8, 8, 64, bs, 512, [1, 2, 15, 16, 17, 100, 255, 256, 257, 300,
                                                                    448, 64, 65, 31, 32, 33], False, 1)
-    assert_close(out, want, dtype, "fused decode")
+    assert_close(out, want, dtype, f"fused decode bs={bs}")
 
 
 @pytest.mark.parametrize("chunk", [0, 256, 512])

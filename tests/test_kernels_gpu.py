@@ -150,7 +150,7 @@ def test_append_then_gather_round_trip(cuda):
 # ------------------------------------------------------------------ paged attention
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
-@pytest.mark.parametrize("bs", [8, 16])
+@pytest.mark.parametrize("bs", [8, 16, 32, 64, 12])  # 32, 64: blocks longer than a wave's trip; 12: general path
 def test_paged_attention_matches_oracle(cuda, dtype, d, bs):
     gen = torch.Generator().manual_seed(100 + d + bs)
     nb, h, maxblk = 256, 4, 12
