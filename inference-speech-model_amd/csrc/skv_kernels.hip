@@ -1412,7 +1412,7 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
   auto s_acc = reinterpret_cast<float (*)[kMqQueries][D + 4]>(s_stage);
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // wave-uniform
   const int g = lane >> 4;   // lane group of the MFMA layouts
   const int n = lane & 15;   // query column (result, P^T) / key or dim row (operands)
   const int h = (int)(blockIdx.x % (uint32_t)p.heads);
@@ -1543,21 +1543,35 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
     __builtin_amdgcn_wave_barrier();
     // Scores of keys base + 16t + 4g + i for query n, masked past the chunk's end.
     float sv[8];
-    float mx = kNegInf;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kk = 16 * t + 4 * g + i;
-        const bool ok = base + kk < t_end && (!PAGED || ((mask >> kk) & 1u));
-        sv[4 * t + i] = ok ? sc[t][i] * p.scale_log2 : kNegInf;
-        mx = fmaxf(mx, sv[4 * t + i]);
-      }
-    mx = fmaxf(mx, xor_lane<16>(mx));
-    mx = fmaxf(mx, xor_lane<32>(mx));
+      for (int i = 0; i < 4; ++i) sv[4 * t + i] = sc[t][i] * p.scale_log2;
+    if (base + STEP > t_end || (PAGED && mask != 0xffffffffu)) {  // wave-uniform: a chunk's last step or an invalid block
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kk = 16 * t + 4 * g + i;
+          const bool ok = base + kk < t_end && (!PAGED || ((mask >> kk) & 1u));
+          sv[4 * t + i] = ok ? sv[4 * t + i] : kNegInf;
+        }
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+    {
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+    }
     const float mn = fmaxf(m, mx);
     const float ref = mn == kNegInf ? 0.f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m - ref);
+    // The accumulators are rescaled only when some query's maximum grew (alpha is exactly 1
+    // for the others).
+    const bool rescale = __builtin_amdgcn_ballot_w64(mn != m) != 0;
     m = mn;
     l *= alpha;
     // P^T operand. fp16 rounds P once (unit roundoff 2^-11) and the row sums add the rounded
@@ -1579,9 +1593,12 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
     }
     const uint4 pt = make_uint4(pw[0], pw[1], pw[2], pw[3]);
     const uint4 prt = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+    if (rescale) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+    }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      acc[db] *= alpha;
       acc[db] = mfma_16x16x32<DT>(vt[db], pt, acc[db]);
       if constexpr (DT == SKV_BF16) acc[db] = mfma_16x16x32<DT>(vt[db], prt, acc[db]);
     }
