@@ -224,7 +224,7 @@ def paged_sets(torch, native, dev, dtype, batch, heads, d, bs, nb, max_ctx, seed
 
 def host_cpu():
     """(threads torch uses, CPU model, logical CPUs the OS reports). The threads are torch's own count,
-    i.e. OMP_NUM_THREADS where it is set (the GPU box's share of the host), else every core."""
+    i.e. OMP_NUM_THREADS where it is set (the process's share of the host), else every core."""
     import torch
 
     model = "unknown"

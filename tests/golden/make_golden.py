@@ -10,7 +10,8 @@ tests/golden/whisper_tiny_golden.npz (numpy arrays only, no pickles):
     greedy loop with the contiguous past  -> greedy_tokens, greedy_logits
     decode_step(prompt, encoder_hidden_states=...) -> proj_logits
 The oracle (oracle/decoder.py) is checked against this file by
-tests/test_decoder_oracle.py. Nothing on the GPU box reads the reference.
+tests/test_decoder_oracle.py. No test, benchmark or library code reads the reference;
+the tests read only this file.
 """
 import json
 import os

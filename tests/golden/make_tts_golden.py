@@ -18,7 +18,7 @@ tests/golden/tts_small_golden.npz (numpy arrays only, no pickles):
     engine_blocks           allocated / free block counts after the run
 The oracle (oracle/tts.py) is checked against this file by
 tests/test_tts_oracle.py, and the HIP engine by tests/test_tts_gpu.py.
-Nothing on the GPU box reads the reference.
+No test, benchmark or library code reads the reference; the tests read only this file.
 """
 import json
 import os
