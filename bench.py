@@ -247,7 +247,7 @@ def baseline_record(value, unit, sample, **extra):
 
 
 def cpu_baseline(s, a, scale, budget_s):
-    """The config-2 step on the host: append + block-table gather into a zero-padded batch + masked
+    """The paged-attention microbench step (fp16, 32 heads, batch 64) on the host: append + block-table gather into a zero-padded batch + masked
     attention in float32 torch on torch's threads (oracle/cpu_path.paged_attention_step). value is
     the GPU workload's algorithmic bytes (fp16 element size) per CPU call time, so the two values
     compare as the inverse of their times."""
@@ -274,7 +274,7 @@ def cpu_baseline(s, a, scale, budget_s):
     times.sort()
     med = times[len(times) // 2]
     return baseline_record(round(nbytes / med / 1e9, 4), "GB/s",
-                           f"{len(times)} calls of the whole config-2 batch (B={a.batch}, fused append + gather + "
+                           f"{len(times)} calls of the whole microbench batch (B={a.batch}, fused append + gather + "
                            f"attention), median {med * 1e3:.2f} ms per call",
                            ms_per_step=round(med * 1e3, 3))
 
@@ -788,7 +788,7 @@ def config1_decode(torch, dev, a):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; multi-GPU runs are not part of it",
+        print(json.dumps({"error": "bench.py measures one GPU only; multi-GPU runs are not part of it",
                           "n_gpus": a.gpus}))
         sys.exit(2)
     import torch
@@ -834,7 +834,7 @@ def main():
     native.lib()
     # The large-v3 kernel legs run first, while the process holds only their own allocations: the
     # same large-v3 paged launch measured up to 4% slower after the engine runs (models, pools and
-    # captured graphs that come and go) and ~1% slower after the config-2 sets.
+    # captured graphs that come and go) and ~1% slower after the fp16 microbench sets.
     legs = {}
     if not a.no_large_v3:
         legs.update(large_v3_kernels(torch, native, dev, a))

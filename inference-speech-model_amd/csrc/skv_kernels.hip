@@ -656,7 +656,7 @@ struct AttnParams {
 #define SKV_ATTN_SUB 64  // most keys one wave loads per loop trip over contiguous K/V
 #endif
 // Paged K/V take shorter trips: a (row, head) ends with finer steps, which shortens
-// the launch's tail (large-v3 batch 64: 14.97 -> 14.61 us, config 2: 21.6 -> 21.3 us),
+// the launch's tail (large-v3 batch 64: 14.97 -> 14.61 us, fp16 32 heads batch 64: 21.6 -> 21.3 us),
 // while the contiguous cross-attention rows (1500 keys each) keep more rows in flight
 // per lane (74.2 -> 73.4 us with 64-key trips). Both are powers of two, and 64 is a
 // multiple of 32, so a chunk sized for the contiguous trip fits the paged one.

@@ -17,7 +17,7 @@ written from the reference's source text (file:line cited per function):
                       baseline bench.py times on the host cores.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may import
-anything from this package, and only as the checker (or, in bench.py, as the
+anything from this package, and only to check results (or, in bench.py, as the
 timed CPU baseline). The product path (speech_serving) never imports it.
 
 Pinning: every oracle function is checked (tests/test_oracle.py,

@@ -183,8 +183,8 @@ def test_paged_attention_config2_full_size(cuda):
     out = native.paged_attention(q, kp, vp, tables.to(cuda), ctx.to(torch.int32).to(cuda), 448, 1 / 8.0)
     torch.cuda.synchronize()
     want = O.paged_attention(f64(q)[:, None], f64(kp), f64(vp), tables.numpy(), ctx.tolist(), 1 / 8.0)[:, 0]
-    err = assert_close(out, want, torch.float16, "config2")
-    print(f"config2 paged attention max abs err {err:.3e}")
+    err = assert_close(out, want, torch.float16, "fp16 H32 B64 microbench")
+    print(f"fp16 H32 B64 microbench paged attention max abs err {err:.3e}")
 
 
 @pytest.mark.parametrize("bsz,h", [(20, 20), (13, 31), (64, 20), (3, 2), (100, 3)])
