@@ -1675,8 +1675,8 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
 // hands its state to part 0 through LDS at the end. The split puts 4 waves on each
 // SIMD (at most 128 VGPRs each) where one part alone would leave 2: the per-step chain
 // (products, softmax, products) is latency-bound, not issue-bound. Each wave runs
-// the same products as mq_attention_kernel on each 32-key half of the shared step
-// (the second half's score products do not wait for the first half's softmax).
+// the same products as mq_attention_kernel on each 32-key half of the shared step; both
+// halves' score products issue before the first half's softmax, so they overlap it.
 // Steps are double-buffered in LDS (80 KB per workgroup) with one barrier per step
 // that orders LDS only; every wave keeps the next step's global loads in flight (16
 // key rows of K and of V, 8 lanes per 128-byte row) and reads their block ids with
@@ -1831,18 +1831,20 @@ mqt_attention_kernel(AttnParams p) {
   f32x4 l4 = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint4 ones = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
 
-  // One 32-key half of the staged step; keys whose bit is clear score -inf.
-  auto compute = [&](int buf, int half, uint32_t bits) __attribute__((always_inline)) {
+  // Scores of one 32-key half of the staged step (K operand of tile t, slab s: key 16t + n,
+  // dims 32s + 8g .. +8).
+  auto scores = [&](int buf, int half, f32x4 (&sc)[2]) __attribute__((always_inline)) {
     const char* lds_k = s_tile[buf] + half * STEP * kRowPad;
-    const char* lds_v = s_tile[buf] + LSTEP * kRowPad + half * STEP * kRowPad;
-    // K operand of tile t, slab s: key 16t + n, dims 32s + 8g .. +8.
-    f32x4 sc[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const char* row = lds_k + (16 * t + n) * kRowPad + 16 * g;
       sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row), qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
       sc[t] = mfma_16x16x32<DT>(*reinterpret_cast<const uint4*>(row + 64), qf[1], sc[t]);
     }
+  };
+  // Softmax and PV products of one half; keys whose bit is clear score -inf.
+  auto compute = [&](int buf, int half, const f32x4 (&sc)[2], uint32_t bits) __attribute__((always_inline)) {
+    const char* lds_v = s_tile[buf] + LSTEP * kRowPad + half * STEP * kRowPad;
     uint4 vt[4];
     {
       const char* row_a = lds_v + vt_key * kRowPad + vt_col;
@@ -1932,8 +1934,11 @@ mqt_attention_kernel(AttnParams p) {
     const uint64_t bits = pbits[SLOT];
     if (st + 1 < nsteps) stage((st + 1) & 1, kr[SLOT ^ 1], vr[SLOT ^ 1]);
     pbits[SLOT] = issue(st0 + st + 2, kr[SLOT], vr[SLOT]);
-    compute(st & 1, 0, (uint32_t)bits);
-    if ((uint32_t)(bits >> 32) != 0u) compute(st & 1, 1, (uint32_t)(bits >> 32));  // a half with no key changes nothing
+    f32x4 sc0[2], sc1[2];
+    scores(st & 1, 0, sc0);
+    scores(st & 1, 1, sc1);  // issued before the first half's softmax, so the two overlap
+    compute(st & 1, 0, sc0, (uint32_t)bits);
+    compute(st & 1, 1, sc1, (uint32_t)(bits >> 32));  // a half with no key changes nothing
     lds_barrier();
   };
   for (int st = 0; st < nsteps; st += 2) {
