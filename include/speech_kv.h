@@ -204,8 +204,9 @@ SKV_API int32_t skv_default_chunk_tokens(int32_t rows, int32_t num_heads, int32_
  * no fused append (attention over an encoder table), head_dim 64, fp16/bf16 and a
  * power-of-two block size of at least 8 run every 16 queries of a row against one
  * read of its blocks, with both products on the matrix cores; with 64 or more
- * queries per row and enough (row, head, 64-query) workgroups to fill the GPU,
- * every 64 queries share one read of the blocks staged in LDS.
+ * queries per row and (row, head, 64-query) workgroups for at least three quarters
+ * of the GPU's compute units, every 64 queries share one read of the blocks staged
+ * in LDS.
  * Row order: the launch spreads (row, head) items over the compute units in a fixed
  * order that balances their bytes when rows come longest-first (as the scheduler lays
  * out its decode batch); rows in arbitrary order give correct results but an uneven
@@ -263,7 +264,7 @@ SKV_API int skv_paged_attention_noalloc(const void* q, int64_t q_stride_b, int64
  * (a prompt's cross-attention), head_dim 64 and fp16/bf16 run every 16 queries of
  * a row against one read of its K/V, with both products on the matrix cores (every
  * 64 queries, staged in LDS, when rows carry 64 or more queries and the
- * (row, head, 64-query) workgroups fill the GPU).
+ * (row, head, 64-query) workgroups cover at least three quarters of the GPU).
  * Reference: models.py:167-203, :468-479, :126-165 (contiguous past).
  */
 SKV_API int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,

@@ -2177,11 +2177,15 @@ void launch_mqt(int32_t dtype, const AttnParams& p, hipStream_t s) {
 }
 
 // Whether the 64-query kernel serves a multi-query launch: enough queries per row,
-// enough (row, head, 64 queries) workgroups to fill the GPU without splitting keys
-// across workgroups, and a positive scale (its maximum is taken on unscaled scores).
+// (row, head, 64 queries) workgroups for at least three quarters of the compute units
+// (it does not split keys across workgroups; below that the 16-query kernel, which
+// does, is faster: encoder attention over 1500 bf16 positions, 6 heads (144
+// workgroups) 20.4 vs 20.7 us, 8 heads (192) 23.2 vs 21.2 us, 20 heads over 750
+// positions (240) 18.0 vs 13.4 us), and a positive scale (its maximum is taken on
+// unscaled scores).
 bool use_mqt(const AttnParams& p) {
   return p.qlen >= kMqtQueries && p.scale_log2 > 0.f &&
-         (int64_t)p.batch * p.heads * cdiv(p.qlen, kMqtQueries) >= device_cu_count() &&
+         4 * (int64_t)p.batch * p.heads * cdiv(p.qlen, kMqtQueries) >= 3 * (int64_t)device_cu_count() &&
          (int64_t)p.heads * cdiv(p.qlen, kMqtQueries) <= 0x7fffffff;
 }
 
