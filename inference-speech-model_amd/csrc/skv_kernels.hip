@@ -2510,9 +2510,20 @@ int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
                              o_stride_b, o_stride_q, o_stride_h, ctx_lens, batch, q_len, num_heads, num_kv_heads,
                              head_dim, max_ctx, scale, causal, dtype, chunk_tokens, workspace, workspace_bytes);
   if (rc != SKV_OK) return rc;
-  if (p.chunk / block_size + 2 > kMaxChunkBlocks)
-    return fail(SKV_EINVAL, "skv_paged_attention: chunk_tokens %d spans more than %d blocks of %d", p.chunk,
-                kMaxChunkBlocks - 2, block_size);
+  // The general paged path (a block size that is not a power of two of at least one load
+  // instruction's keys, or a pool past the 32-bit buffer range) stages a chunk's block ids in
+  // kMaxChunkBlocks LDS slots; the fast path and the multi-query kernels read block ids with
+  // scalar loads and take chunks of any length.
+  {
+    const int epl = 16 / elt_bytes(dtype);
+    const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
+    const int64_t kv_bytes = (int64_t)num_blocks * block_size * ((int64_t)num_kv_heads * head_dim / epl) * 16;
+    const bool fast = kv_bytes <= kBufLimit && bs_shift >= 0 && (1 << bs_shift) >= 64 * epl / head_dim;
+    if (!fast && p.chunk / block_size + 2 > kMaxChunkBlocks)
+      return fail(SKV_EINVAL,
+                  "skv_paged_attention: chunk_tokens %d spans more than %d blocks of %d (pass a smaller chunk_tokens)",
+                  p.chunk, kMaxChunkBlocks - 2, block_size);
+  }
   if (k_new) {
     const int epl = 16 / elt_bytes(dtype);
     if (!aligned16(k_new) || !aligned16(v_new) || new_stride_b % epl || new_stride_q % epl || new_stride_h % epl)

@@ -148,6 +148,37 @@ def test_append_then_gather_round_trip(cuda):
 
 
 # ------------------------------------------------------------------ paged attention
+@pytest.mark.parametrize("bs,max_ctx", [(16, 4100), (8, 2100), (12, 4100)])
+def test_paged_attention_long_context_default_chunk(cuda, bs, max_ctx):
+    """1024 (row, head) pairs take one chunk per row by default; at these contexts that chunk spans more
+    than the general path's 254 staged block ids. Power-of-two blocks (the fast path, block ids read per
+    trip) attend over it; a block size of 12 (the general path) reports the limit instead."""
+    gen = torch.Generator().manual_seed(bs + max_ctx)
+    bsz, h, d, dtype = 64, 16, 64, torch.bfloat16
+    lens = [max_ctx, (max_ctx * 3) // 4] + torch.randint(1, 41, (bsz - 2,), generator=gen).tolist()
+    maxblk = -(-max_ctx // bs)
+    need = [-(-n // bs) for n in lens]
+    nb = sum(need) + 8
+    kp, vp = make_pool(gen, nb, bs, h, d, dtype, cuda)
+    perm = torch.randperm(nb, generator=gen).to(torch.int32)
+    tables = torch.full((bsz, maxblk), -1, dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(need):
+        tables[i, :n] = perm[at:at + n]
+        at += n
+    q = torch.randn(bsz, h, d, generator=gen).to(cuda, dtype)
+    call = lambda: native.paged_attention(q, kp, vp, tables.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
+                                          max_ctx, 0.125)
+    if bs & (bs - 1):
+        with pytest.raises(RuntimeError, match="chunk_tokens"):
+            call()
+        return
+    out = call()
+    torch.cuda.synchronize()
+    want = O.paged_attention(f64(q)[:, None], f64(kp), f64(vp), tables.numpy(), lens, 0.125)[:, 0]
+    assert_close(out, want, dtype, f"long context bs={bs} max_ctx={max_ctx}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
 @pytest.mark.parametrize("bs", [8, 16, 32, 64, 12])  # 32, 64: blocks longer than a wave's trip; 12: general path
