@@ -56,9 +56,17 @@ def test_default_chunk():
     # rounded up to whole 4-wave passes (fp16 D=64: 4 waves x 64 keys = 256).
     assert lib.skv_default_chunk_tokens(64, 32, 64, 448, native.SKV_F16) == 512
     assert lib.skv_default_chunk_tokens(64, 20, 64, 1500, native.SKV_BF16) == 1536
-    # Few pairs: split the keys so that ~1024 workgroups run.
+    # Few pairs over long keys: split the keys so that ~1024 workgroups run.
     c = lib.skv_default_chunk_tokens(1, 20, 64, 1500, native.SKV_BF16)
     assert c == 256 and 20 * -(-1500 // c) <= 1024
+    assert lib.skv_default_chunk_tokens(8, 20, 64, 4096, native.SKV_BF16) == 768
+    # A (row, head) of at most 128 KB of K and V (512 keys at bf16 D=64) is never split ...
+    assert lib.skv_default_chunk_tokens(1, 20, 64, 512, native.SKV_BF16) == 512
+    assert lib.skv_default_chunk_tokens(1, 20, 64, 513, native.SKV_BF16) == 256
+    # ... nor is one of at most 512 KB when there are 128 or more pairs.
+    assert lib.skv_default_chunk_tokens(8, 20, 64, 1500, native.SKV_BF16) == 1536
+    assert lib.skv_default_chunk_tokens(6, 20, 64, 1500, native.SKV_BF16) == 256
+    assert lib.skv_default_chunk_tokens(8, 20, 64, 2049, native.SKV_BF16) == 512
     # fp32 D=64: 4 rows x 8 = 32 keys per wave -> 128-key passes
     assert lib.skv_default_chunk_tokens(1, 1, 64, 10, native.SKV_F32) == 128
 
