@@ -164,6 +164,11 @@ template <int OFF> __device__ __forceinline__ float xor_lane(float x) {
   }
 }
 
+// Maximum of two scores (or running maxima), NaN-propagating: gfx950's v_maximum3_f32, one
+// instruction. fmaxf (IEEE maxNum) first quiets each operand the compiler cannot prove
+// canonical (a cross-lane result, a loop-carried value): one extra instruction per operand.
+__device__ __forceinline__ float max_score(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Workgroup barrier that orders LDS only. __syncthreads() is also a release of
 // global memory, which makes every wave wait for all of its outstanding global
 // loads and stores before the barrier; a loop that stages tiles through LDS

@@ -1559,14 +1559,14 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
     }
     float mx = kNegInf;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+    for (int i = 0; i < 8; ++i) mx = max_score(mx, sv[i]);
     {
       const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      mx = max_score(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      mx = max_score(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
     }
-    const float mn = fmaxf(m, mx);
+    const float mn = max_score(m, mx);
     const float ref = mn == kNegInf ? 0.f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m - ref);
     // The accumulators are rescaled only when some query's maximum grew (alpha is exactly 1
@@ -1868,16 +1868,16 @@ mqt_attention_kernel(AttnParams p) {
     }
     float mx = kNegInf;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sv[i]);
+    for (int i = 0; i < 8; ++i) mx = max_score(mx, sv[i]);
     // Maximum over the 4 lane groups: a permlane swap of a register with itself leaves
     // a lane's own value in one result and its partner's in the other.
     {
       const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      mx = max_score(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      mx = max_score(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
     }
-    const float mn = fmaxf(m, mx * p.scale_log2);
+    const float mn = max_score(m, mx * p.scale_log2);
     const float ref = mn == kNegInf ? 0.f : mn;
     const float alpha = __builtin_amdgcn_exp2f(m - ref);
     // The accumulators are rescaled only when some query's maximum grew (alpha is
