@@ -1391,6 +1391,13 @@ __device__ __forceinline__ uint4 vt_operand(const char* row_a, const char* row_b
 }
 
 constexpr int kMqQueries = 16;  // queries per tile (the MFMA's N)
+// Lazy rescaling of the matrix-core kernels' online softmax: a wave's reference maximum
+// (and with it the accumulators' scale) moves only when some query's step maximum exceeds it
+// by more than this (log2 units), so the weights stay below 2^8, which the fp32 sums and the
+// fp16/bf16 P operands hold at unchanged relative precision. With 16 queries per wave some
+// query's maximum grows in most steps: rescaling at every growth multiplied the accumulators
+// almost every step.
+constexpr float kLazyMaxLog2 = 8.f;
 static_assert(kWaves == 4, "mq_attention_kernel: each of the 4 waves finalises one 16-dim block");
 
 // 3 waves per SIMD: the register budget that holds the next step's loads in flight without
@@ -1566,14 +1573,16 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
       mx = max_score(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
     }
-    const float mn = max_score(m, mx);
-    const float ref = mn == kNegInf ? 0.f : mn;
-    const float alpha = __builtin_amdgcn_exp2f(m - ref);
-    // The accumulators are rescaled only when some query's maximum grew (alpha is exactly 1
-    // for the others).
-    const bool rescale = __builtin_amdgcn_ballot_w64(mn != m) != 0;
-    m = mn;
-    l *= alpha;
+    // Lazy rescaling (kLazyMaxLog2).
+    if (__builtin_amdgcn_ballot_w64(mx > m + kLazyMaxLog2) != 0) {  // wave-uniform
+      const float mn = max_score(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - (mn == kNegInf ? 0.f : mn));
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+      l *= alpha;
+      m = mn;
+    }
+    const float ref = m == kNegInf ? 0.f : m;
     // P^T operand. fp16 rounds P once (unit roundoff 2^-11) and the row sums add the rounded
     // values; bf16 (2^-8) splits P into a rounded head and the rounded remainder, two products
     // with the same V^T, so the weights keep ~16 bits and the sums use P itself.
@@ -1593,10 +1602,6 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
     }
     const uint4 pt = make_uint4(pw[0], pw[1], pw[2], pw[3]);
     const uint4 prt = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-    if (rescale) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-    }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       acc[db] = mfma_16x16x32<DT>(vt[db], pt, acc[db]);
@@ -1877,17 +1882,20 @@ mqt_attention_kernel(AttnParams p) {
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
       mx = max_score(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
     }
-    const float mn = max_score(m, mx * p.scale_log2);
-    const float ref = mn == kNegInf ? 0.f : mn;
-    const float alpha = __builtin_amdgcn_exp2f(m - ref);
-    // The accumulators are rescaled only when some query's maximum grew (alpha is
-    // exactly 1 for the others): past the first steps most steps skip it.
-    const bool rescale = __builtin_amdgcn_ballot_w64(mn != m) != 0;
-    m = mn;
-    if constexpr (kOnesSum)
-      l4 *= alpha;
-    else
-      l *= alpha;
+    // Lazy rescaling (kLazyMaxLog2).
+    const float smx = mx * p.scale_log2;
+    if (__builtin_amdgcn_ballot_w64(smx > m + kLazyMaxLog2) != 0) {  // wave-uniform
+      const float mn = max_score(m, smx);
+      const float alpha = __builtin_amdgcn_exp2f(m - (mn == kNegInf ? 0.f : mn));
+#pragma unroll
+      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+      if constexpr (kOnesSum)
+        l4 *= alpha;
+      else
+        l *= alpha;
+      m = mn;
+    }
+    const float ref = m == kNegInf ? 0.f : m;
     // P^T operand, as in mq_attention_kernel: fp16 rounds P once and sums the rounded
     // values; bf16 adds the product of the rounded remainder.
     uint32_t pw[4], pr[4];
@@ -1904,10 +1912,6 @@ mqt_attention_kernel(AttnParams p) {
     }
     const uint4 pt = make_uint4(pw[0], pw[1], pw[2], pw[3]);
     const uint4 prt = make_uint4(pr[0], pr[1], pr[2], pr[3]);
-    if (rescale) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-    }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       acc[db] = mfma_16x16x32<DT>(vt[db], pt, acc[db]);

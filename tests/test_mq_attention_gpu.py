@@ -170,6 +170,28 @@ def test_many_queries_non_positive_scale(cuda, scale):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("qlen,rows", [(16, 4), (64, 16)])  # the 16-query kernel, the 64-query kernel
+def test_rising_scores_rescale_mid_row(cuda, dtype, qlen, rows):
+    """Scores that keep rising along the keys (a ramp up to ~58 in log2 units, steeper for later
+    queries) and a spike at key 1400: both kernels move their reference maximum only when a step's
+    maximum exceeds it by more than 8 (log2 units), so these rows rescale their accumulators several
+    times mid-row and once near the end, with weights up to 2^8 in between."""
+    h = 20 if qlen == 64 else 4
+    assert mqt_selected(rows, h, qlen) == (qlen == 64)
+    lens = ([1500, 1401, 1399, 800] * 4)[:rows]
+    slots = list(range(rows))
+    g, q, lens_t, slots_t, layer = cross_case(cuda, torch.float32, qlen, 140 + qlen, lens, slots, h=h)
+    g[:, layer, 0, :, :, 0] = torch.linspace(0.0, 40.0, 1500, device=cuda)
+    g[:, layer, 0, :, 1400, 0] = 60.0
+    q[..., 0] = torch.linspace(0.5, 8.0, qlen, device=cuda)[None, :, None]
+    g, q = g.to(dtype), q.to(dtype)
+    out = native.dense_attention(q, g[:, layer, 0], g[:, layer, 1], lens_t, 1500, 0.125, slot_ids=slots_t)
+    want = O.dense_attention(f64(q), f64(g[:, layer, 0]), f64(g[:, layer, 1]), lens, 0.125, slot_ids=slots)
+    err = check(out, want, dtype, f"rising scores, q_len {qlen}")
+    print(f"rising scores q_len {qlen} {dtype}: max err {err:.2e}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("kv_heads", [20, 4])
 def test_encoder_attention_shape_paged(cuda, dtype, kv_heads):
     """The encoder-attention shape on the 64-query kernel: 1500 queries x 20 heads over one table of 94
