@@ -1494,6 +1494,7 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
   const int vt_col = 8 * (lane & 3);
 
   float m = kNegInf, l = 0.f;  // this lane's query n; l sums the keys of this lane group
+  float ref = 0.f;             // m, or 0 while m is -inf: the exponents' offset
   f32x4 acc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1567,22 +1568,22 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
     float mx = kNegInf;
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = max_score(mx, sv[i]);
-    {
+    // Lazy rescaling (kLazyMaxLog2). A lane's own 8 keys decide whether the reference moves;
+    // only then is the maximum taken over the query's 4 lane groups (a permlane swap of a
+    // register with itself leaves a lane's own value in one result, its partner's in the other).
+    if (__builtin_amdgcn_ballot_w64(mx > m + kLazyMaxLog2) != 0) {  // wave-uniform
       const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
       mx = max_score(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
       mx = max_score(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-    }
-    // Lazy rescaling (kLazyMaxLog2).
-    if (__builtin_amdgcn_ballot_w64(mx > m + kLazyMaxLog2) != 0) {  // wave-uniform
       const float mn = max_score(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m - (mn == kNegInf ? 0.f : mn));
+      ref = mn == kNegInf ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m - ref);
 #pragma unroll
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
       l *= alpha;
       m = mn;
     }
-    const float ref = m == kNegInf ? 0.f : m;
     // P^T operand. fp16 rounds P once (unit roundoff 2^-11) and the row sums add the rounded
     // values; bf16 (2^-8) splits P into a rounded head and the rounded remainder, two products
     // with the same V^T, so the weights keep ~16 bits and the sums use P itself.
@@ -1646,11 +1647,11 @@ mq_attention_kernel(AttnParams p, int32_t qtiles) {
   float M = kNegInf;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][n]);
-  const float ref = M == kNegInf ? 0.f : M;
+  const float mref = M == kNegInf ? 0.f : M;
   float L = 0.f, A[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
-    const float e = __builtin_amdgcn_exp2f(s_m[w][n] - ref);
+    const float e = __builtin_amdgcn_exp2f(s_m[w][n] - mref);
     L += e * s_l[w][n];
 #pragma unroll
     for (int i = 0; i < 4; ++i) A[i] += e * s_acc[w][n][16 * wave + 4 * g + i];
@@ -1826,6 +1827,7 @@ mqt_attention_kernel(AttnParams p) {
   const int vt_col = 8 * (lane & 3);
 
   float m = kNegInf, l = 0.f;  // query n's state (m in units of scale * log2 e); l sums this lane group's keys
+  float ref = 0.f;             // m, or 0 while m is -inf: the exponents' offset
   f32x4 acc[4];
 #pragma unroll
   for (int db = 0; db < 4; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1874,19 +1876,17 @@ mqt_attention_kernel(AttnParams p) {
     float mx = kNegInf;
 #pragma unroll
     for (int i = 0; i < 8; ++i) mx = max_score(mx, sv[i]);
-    // Maximum over the 4 lane groups: a permlane swap of a register with itself leaves
-    // a lane's own value in one result and its partner's in the other.
-    {
+    // Lazy rescaling (kLazyMaxLog2). A lane's own 8 keys decide whether the reference moves;
+    // only then is the maximum taken over the query's 4 lane groups (a permlane swap of a
+    // register with itself leaves a lane's own value in one result, its partner's in the other).
+    if (__builtin_amdgcn_ballot_w64(mx * p.scale_log2 > m + kLazyMaxLog2) != 0) {  // wave-uniform
       const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
       mx = max_score(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
       mx = max_score(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-    }
-    // Lazy rescaling (kLazyMaxLog2).
-    const float smx = mx * p.scale_log2;
-    if (__builtin_amdgcn_ballot_w64(smx > m + kLazyMaxLog2) != 0) {  // wave-uniform
-      const float mn = max_score(m, smx);
-      const float alpha = __builtin_amdgcn_exp2f(m - (mn == kNegInf ? 0.f : mn));
+      const float mn = max_score(m, mx * p.scale_log2);
+      ref = mn == kNegInf ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m - ref);
 #pragma unroll
       for (int db = 0; db < 4; ++db) acc[db] *= alpha;
       if constexpr (kOnesSum)
@@ -1895,7 +1895,6 @@ mqt_attention_kernel(AttnParams p) {
         l *= alpha;
       m = mn;
     }
-    const float ref = m == kNegInf ? 0.f : m;
     // P^T operand, as in mq_attention_kernel: fp16 rounds P once and sums the rounded
     // values; bf16 adds the product of the rounded remainder.
     uint32_t pw[4], pr[4];
