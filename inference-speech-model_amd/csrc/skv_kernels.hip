@@ -269,14 +269,18 @@ __global__ __launch_bounds__(256) void cross_copy_kernel(CrossCopyParams p) {
 // the slot is not yet finished, slot_finished[s] = 1 and finished_count += 1.
 // One workgroup per row reads the row as 16-byte vectors of 32-bit words through a
 // buffer descriptor (reads past the row's last word return zeros and are not
-// compared), kArgmaxVecs vectors per thread in flight. A thread visits its elements
-// in increasing index order and keeps the first strictly greater value, so each
-// element costs a compare and two selects; a NaN only sets a flag, and a thread that
-// saw one rescans its elements for the first NaN (NaN counts as the maximum). A
-// 16-bit row that starts in the middle of a word has its first element handled alone.
+// compared), VECS vectors per thread in flight. A thread visits its elements
+// in increasing index order and keeps the first strictly greater value: per element a
+// compare and two selects (the value, and the element's position in the pass, a
+// constant; the position becomes an index once per pass). A NaN-propagating running
+// maximum (one instruction per two elements) flags a NaN, and a thread that saw one
+// rescans its elements for the first NaN (NaN counts as the maximum). A 16-bit row
+// that starts in the middle of a word has its first element handled alone.
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxThreads = 1024;
-constexpr int kArgmaxVecs = 4;  // 16-byte vectors per thread per pass: 32768 16-bit logits
+// 16-byte vectors per thread per pass (VECS): the launch takes the fewest of 1, 2, 4, 7 that
+// cover a row in one pass (7: up to 57344 16-bit logits, so the 51866-entry Whisper vocabulary
+// is one pass); larger rows take several passes of 7.
 
 __device__ __forceinline__ bool argmax_better(float v1, int i1, float v2, int i2) {
   const bool n1 = v1 != v1, n2 = v2 != v2;
@@ -308,7 +312,7 @@ struct SlotFeedback {
   unsigned long long* finished_count;
 };
 
-template <int DT>
+template <int DT, int VECS>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __restrict__ logits, int64_t row_bytes,
                                                                 int32_t vocab, int64_t* __restrict__ out,
                                                                 SlotFeedback f) {
@@ -328,38 +332,61 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
   // -inf resolves to its first index like the others.
   float best = kNegInf;
   int bi = 4 * (int)threadIdx.x < nw ? head + EPW * 4 * (int)threadIdx.x : 0x7fffffff;
-  bool nan_seen = false;
+  float nmax = kNegInf;  // NaN-propagating maximum of the thread's elements: NaN flags a NaN
   // Thread t's vectors: words 4 * (t + kArgmaxThreads * k) .. +3, k = 0, 1, ...
-  constexpr int kPassWords = 4 * kArgmaxThreads * kArgmaxVecs;
+  constexpr int kPassWords = 4 * kArgmaxThreads * VECS;
+  constexpr int kVecElts = 4 * EPW;
   for (int p0 = 0; p0 < nw; p0 += kPassWords) {
-    u32x4 x[kArgmaxVecs];
+    u32x4 x[VECS];
 #pragma unroll
-    for (int k = 0; k < kArgmaxVecs; ++k)
+    for (int k = 0; k < VECS; ++k)
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(
           res, (uint32_t)(p0 + 4 * ((int)threadIdx.x + kArgmaxThreads * k)) * 4u, 0, kBufNt);
+    // The pass's winner is kept as its position k * kVecElts + (EPW * j + e), a constant of
+    // the unrolled loop (-1: none), and turned into an element index once per pass.
+    int pos = -1;
+    auto visit = [&](float v, int at) __attribute__((always_inline)) {
+      const bool gt = v > best;
+      best = gt ? v : best;
+      pos = gt ? at : pos;
+    };
 #pragma unroll
-    for (int k = 0; k < kArgmaxVecs; ++k) {
+    for (int k = 0; k < VECS; ++k) {
       const int w0 = p0 + 4 * ((int)threadIdx.x + kArgmaxThreads * k);
-      const int valid = min(max(nw - w0, 0), 4);  // words of this vector inside the row
+      if (w0 + 4 <= nw) {  // a whole vector inside the row
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4; ++j) {
+          float v[EPW];
 #pragma unroll
-        for (int e = 0; e < EPW; ++e) {
-          float v = word_elt<DT>(x[k][j], e);
-          v = j < valid ? v : kNegInf;
-          const int i = head + EPW * (w0 + j) + e;
-          const bool gt = v > best;
-          best = gt ? v : best;
-          bi = gt ? i : bi;
-          nan_seen |= v != v;
+          for (int e = 0; e < EPW; ++e) v[e] = word_elt<DT>(x[k][j], e);
+          if constexpr (EPW == 2)
+            nmax = max_score(nmax, max_score(v[0], v[1]));
+          else
+            nmax = max_score(nmax, v[0]);
+#pragma unroll
+          for (int e = 0; e < EPW; ++e) visit(v[e], k * kVecElts + EPW * j + e);
         }
+      } else if (w0 < nw) {  // the row's last vector, partly past its end
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < EPW; ++e) {
+            const float v = j < nw - w0 ? word_elt<DT>(x[k][j], e) : kNegInf;
+            nmax = max_score(nmax, v);
+            visit(v, k * kVecElts + EPW * j + e);
+          }
       }
     }
+    if (pos >= 0) {
+      const int k = pos / kVecElts;
+      bi = head + EPW * (p0 + 4 * ((int)threadIdx.x + kArgmaxThreads * k)) + (pos - k * kVecElts);
+    }
   }
+  const bool nan_seen = nmax != nmax;
   if (nan_seen) {  // rare: the first NaN among this thread's elements wins
     int ni = 0x7fffffff;
     for (int p0 = 0; p0 < nw; p0 += kPassWords)
-      for (int k = 0; k < kArgmaxVecs; ++k) {
+      for (int k = 0; k < VECS; ++k) {
         const int w0 = p0 + 4 * ((int)threadIdx.x + kArgmaxThreads * k);
         const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(res, (uint32_t)w0 * 4u, 0, kBufNt);
         for (int j = 0; j < 4; ++j)
@@ -424,6 +451,18 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
         }
       }
     }
+  }
+}
+
+template <int DT>
+void launch_argmax(int vecs, int32_t rows, hipStream_t s, const char* logits, int64_t rb, int32_t vocab, int64_t* out,
+                   const SlotFeedback& f) {
+  const dim3 grid((uint32_t)rows), block(kArgmaxThreads);
+  switch (vecs) {
+    case 1: hipLaunchKernelGGL((argmax_kernel<DT, 1>), grid, block, 0, s, logits, rb, vocab, out, f); break;
+    case 2: hipLaunchKernelGGL((argmax_kernel<DT, 2>), grid, block, 0, s, logits, rb, vocab, out, f); break;
+    case 4: hipLaunchKernelGGL((argmax_kernel<DT, 4>), grid, block, 0, s, logits, rb, vocab, out, f); break;
+    default: hipLaunchKernelGGL((argmax_kernel<DT, 7>), grid, block, 0, s, logits, rb, vocab, out, f); break;
   }
 }
 
@@ -2393,19 +2432,18 @@ int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int32_t voc
     return fail(SKV_EINVAL, "skv_argmax: null pointer argument");
   SlotFeedback f{row_slots, num_slots, slot_tokens, slot_eos, slot_finished, (unsigned long long*)finished_count};
   const int64_t rb = row_stride * eb;
-  hipStream_t s = (hipStream_t)stream;
+  // 16-byte vectors per thread for one pass over a row (its 32-bit words, rounded up).
+  const int64_t per_thread = cdiv(cdiv((int64_t)vocab * eb, 16), kArgmaxThreads);
+  const int vecs = per_thread <= 1 ? 1 : per_thread <= 2 ? 2 : per_thread <= 4 ? 4 : 7;
   switch (dtype) {
     case SKV_F32:
-      hipLaunchKernelGGL(argmax_kernel<SKV_F32>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
-                         out_tokens, f);
+      launch_argmax<SKV_F32>(vecs, rows, (hipStream_t)stream, (const char*)logits, rb, vocab, out_tokens, f);
       break;
     case SKV_F16:
-      hipLaunchKernelGGL(argmax_kernel<SKV_F16>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
-                         out_tokens, f);
+      launch_argmax<SKV_F16>(vecs, rows, (hipStream_t)stream, (const char*)logits, rb, vocab, out_tokens, f);
       break;
     default:
-      hipLaunchKernelGGL(argmax_kernel<SKV_BF16>, dim3(rows), dim3(kArgmaxThreads), 0, s, (const char*)logits, rb, vocab,
-                         out_tokens, f);
+      launch_argmax<SKV_BF16>(vecs, rows, (hipStream_t)stream, (const char*)logits, rb, vocab, out_tokens, f);
       break;
   }
   return check_launch("skv_argmax");

@@ -12,7 +12,9 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("vocab", [1, 100, 51865, 51866])
+# 16-byte vectors per thread: 1, 100: one; 12345: two (16-bit logits) or four (fp32); 30000: four
+# (16-bit) or two passes of seven (fp32); 51865, 51866: one pass of seven (16-bit) or two (fp32).
+@pytest.mark.parametrize("vocab", [1, 100, 12345, 30000, 51865, 51866])
 def test_argmax_matches_numpy_first_max(cuda, dtype, vocab):
     gen = torch.Generator().manual_seed(vocab)
     rows = 7
@@ -120,7 +122,7 @@ def test_argmax_in_graph_replays(cuda):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("vocab", [2, 3, 4097, 51865])
+@pytest.mark.parametrize("vocab", [2, 3, 4097, 12345, 30001, 51865])
 def test_argmax_rows_starting_mid_word(cuda, dtype, vocab):
     # A view one element into each row: every row starts 2 bytes past a 4-byte
     # boundary, so the first element is read alone; odd lengths leave a last one.
