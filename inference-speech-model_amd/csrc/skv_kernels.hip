@@ -816,9 +816,9 @@ __device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off
 // qlen_group: q_len in bits 0-15, query heads per KV head in bits 16-31.
 // flags: bit 0 grid3d, bit 1 snake order, bit 2 causal, bits 8-15 cu_shift,
 // bits 16-23 log2(block size) (the fast path's power-of-two block size).
-// Paged launches hold 5 workgroups per CU (the large decode batches fill one
-// resident generation), so the paged variants are kept within the register
-// budget of 5 waves per SIMD.
+// The paged variants are built for at least 5 waves per SIMD, the register
+// budget of 5 resident workgroups per CU (a large decode batch's launch is one
+// resident generation); at head_dim 64 they take 60-62 VGPRs.
 template <int DT, int D, bool PAGED, bool FAST>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAGED ? 5 : 1))) void attention_kernel(
     const int32_t* __restrict__ a_tables, const int32_t* __restrict__ a_lens, const int32_t* __restrict__ a_trows,
