@@ -13,8 +13,9 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 # 16-byte vectors per thread: 1, 100: one; 12345: two (16-bit logits) or four (fp32); 30000: four
-# (16-bit) or two passes of seven (fp32); 51865, 51866: one pass of seven (16-bit) or two (fp32).
-@pytest.mark.parametrize("vocab", [1, 100, 12345, 30000, 51865, 51866])
+# (16-bit) or two passes of seven (fp32); 51865, 51866: one pass of seven (16-bit) or two (fp32);
+# 100003: two passes of seven (16-bit) or four (fp32).
+@pytest.mark.parametrize("vocab", [1, 100, 12345, 30000, 51865, 51866, 100003])
 def test_argmax_matches_numpy_first_max(cuda, dtype, vocab):
     gen = torch.Generator().manual_seed(vocab)
     rows = 7
