@@ -147,6 +147,30 @@ def test_append_then_gather_round_trip(cuda):
     assert torch.equal(ko[0], src_k.permute(1, 0, 2)) and torch.equal(vo[0], src_v.permute(1, 0, 2))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("bs", [16, 12])  # the fast path (block ids per trip), the general path (staged in LDS)
+def test_paged_attention_few_rows_long_context_default_split(cuda, dtype, bs):
+    """2 rows x 4 heads over 4000 / 1700 keys: too few (row, head) pairs for the GPU and too many keys for one
+    workgroup each, so the default chunk splits the keys (partials in the workspace, combined by the merge
+    launch); with the new key appended through the table."""
+    gen = torch.Generator().manual_seed(300 + bs)
+    h, d, lens = 4, 64, [4000, 1700]
+    assert native.attention_workspace_bytes(len(lens), h, d, max(lens), dtype) > 0  # the keys are split
+    maxblk = -(-max(lens) // bs)
+    nb = 2 * maxblk + 4
+    kp, vp = make_pool(gen, nb, bs, h, d, dtype, cuda)
+    tables = make_tables(gen, len(lens), nb, maxblk)
+    q = torch.randn(len(lens), h, d, generator=gen).to(cuda, dtype)
+    kn = torch.randn(len(lens), h, d, generator=gen).to(cuda, dtype)
+    vn = torch.randn(len(lens), h, d, generator=gen).to(cuda, dtype)
+    out = native.paged_attention(q, kp, vp, tables.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
+                                 max(lens), 0.125, k_new=kn, v_new=vn)
+    torch.cuda.synchronize()
+    want = O.paged_attention(f64(q)[:, None], f64(kp), f64(vp), tables.numpy(), lens, 0.125)[:, 0]
+    err = assert_close(out, want, dtype, f"default split, block size {bs}")
+    print(f"few rows, long context, {dtype}, block size {bs}: max err {err:.2e}")
+
+
 # ------------------------------------------------------------------ paged attention
 @pytest.mark.parametrize("bs,max_ctx", [(16, 4100), (8, 2100), (12, 4100)])
 def test_paged_attention_long_context_default_chunk(cuda, bs, max_ctx):
