@@ -179,9 +179,23 @@ SKV_API int skv_argmax(const void* logits, int64_t row_stride, int32_t rows, int
 SKV_API int64_t skv_attention_workspace_bytes(int32_t rows, int32_t num_heads, int32_t head_dim,
                                       int32_t max_len, int32_t chunk_tokens, int32_t dtype);
 
-/* Chunk size the library uses when chunk_tokens == 0. */
+/* Chunk size skv_dense_attention uses when chunk_tokens == 0. */
 SKV_API int32_t skv_default_chunk_tokens(int32_t rows, int32_t num_heads, int32_t head_dim,
                                  int32_t max_len, int32_t dtype);
+
+/*
+ * Chunk size skv_paged_attention uses when chunk_tokens == 0 for pools of num_blocks
+ * blocks of block_size tokens: skv_default_chunk_tokens, except that pools read
+ * through staged block ids (a block size that is not a power of two of at least
+ * 64 * (16 / element bytes) / head_dim keys, or a pool past 2 GiB) keep a chunk
+ * within 254 blocks. Pass it to skv_attention_workspace_bytes to size the
+ * workspace of such a call.
+ * Reference: the block-table walk of scripts/evaluate_paging_variants.py:56-133
+ * (one block id per BLOCK_SIZE keys).
+ */
+SKV_API int32_t skv_paged_chunk_tokens(int32_t rows, int32_t num_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t max_ctx, int32_t dtype,
+                                       int32_t block_size, int32_t num_blocks);
 
 /*
  * skv_paged_attention — softmax(q K^T * scale) V over the paged K/V of each row.

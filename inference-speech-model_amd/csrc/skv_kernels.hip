@@ -2050,7 +2050,9 @@ int sub_tokens(int32_t dtype, int32_t d) {
   return tpi * u;
 }
 
-int32_t pick_chunk(int32_t rows, int32_t heads, int32_t d, int32_t max_len, int32_t dtype) {
+// cap_tokens > 0 bounds the chunk (rounded down to a whole sub-chunk): the general paged
+// path stages a chunk's block ids in kMaxChunkBlocks LDS slots.
+int32_t pick_chunk(int32_t rows, int32_t heads, int32_t d, int32_t max_len, int32_t dtype, int32_t cap_tokens = 0) {
   int sub = sub_tokens(dtype, d);
   if (sub <= 0) sub = 64;
   // A chunk is a whole number of workgroup passes (kWaves sub-chunks). Keep one chunk per
@@ -2075,7 +2077,27 @@ int32_t pick_chunk(int32_t rows, int32_t heads, int32_t d, int32_t max_len, int3
   const int64_t per = cdiv(max_len > 0 ? max_len : 1, nchunks);
   int64_t chunk = cdiv(per, base) * base;
   if (chunk > 16384) chunk = 16384;
+  if (cap_tokens > 0 && chunk > cap_tokens) chunk = cap_tokens >= sub ? (cap_tokens / sub) * sub : sub;
   return (int32_t)chunk;
+}
+
+// Whether a paged call takes the fast path of attention_kernel: the pools fit the 32-bit
+// buffer range and the block size is a power of two of at least the keys one load
+// instruction of a wave covers (64 * elements per 16 bytes / head_dim).
+bool paged_fast(int32_t dtype, int32_t d, int32_t kv_heads, int32_t bs, int32_t nb) {
+  const int eb = elt_bytes(dtype);
+  if (eb == 0 || d <= 0 || bs <= 0 || nb < 0) return false;
+  const int epl = 16 / eb;
+  const int64_t kv_bytes = (int64_t)nb * bs * ((int64_t)kv_heads * d / epl) * 16;
+  return kv_bytes <= kBufLimit && (bs & (bs - 1)) == 0 && bs >= 64 * epl / d;
+}
+
+// Default chunk of a paged call: the general path keeps each chunk within
+// kMaxChunkBlocks - 2 blocks (a chunk that starts mid-block spans one more).
+int32_t paged_chunk(int32_t rows, int32_t heads, int32_t kv_heads, int32_t d, int32_t max_len, int32_t dtype,
+                    int32_t bs, int32_t nb) {
+  const int32_t cap = paged_fast(dtype, d, kv_heads, bs, nb) ? 0 : (kMaxChunkBlocks - 2) * bs;
+  return pick_chunk(rows, heads, d, max_len, dtype, cap);
 }
 
 bool supported_d(int32_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
@@ -2136,8 +2158,7 @@ int dispatch_attention(int32_t dtype, int32_t d, const AttnParams& p, hipStream_
 int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb, int64_t qsq, int64_t qsh,
                       const void* k, const void* v, void* out, int64_t osb, int64_t osq, int64_t osh,
                       const int32_t* lens, int32_t batch, int32_t q_len, int32_t heads, int32_t kv_heads,
-                      int32_t d, int32_t max_len, float scale, int32_t causal, int32_t dtype, int32_t chunk,
-                      void* ws, int64_t ws_bytes) {
+                      int32_t d, int32_t max_len, float scale, int32_t causal, int32_t dtype, int32_t chunk) {
   const int eb = elt_bytes(dtype);
   if (eb == 0) return fail(SKV_EDTYPE, "%s: unknown dtype %d", who, dtype);
   if (!supported_d(d)) return fail(SKV_EINVAL, "%s: head_dim %d not in {16,32,64,128}", who, d);
@@ -2159,10 +2180,6 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
   if ((int64_t)batch * q_len * heads * 64 * kWaves >= ((int64_t)1 << 32) || nchunk_max > 65535)
     return fail(SKV_EINVAL, "%s: launch too large (rows*heads=%lld, chunks=%d)", who,
                 (long long)batch * q_len * heads, nchunk_max);
-  const int64_t need = workspace_bytes((int64_t)batch * q_len, heads, d, nchunk_max);
-  if (need > 0 && (!ws || ws_bytes < need || !aligned16(ws)))
-    return fail(SKV_EWORKSPACE, "%s: workspace needs %lld bytes (16-byte aligned), got %lld", who, (long long)need,
-                (long long)ws_bytes);
   p.q = (const uint4*)q;
   p.qsb = qsb / epl;
   p.qsq = qsq / epl;
@@ -2193,6 +2210,17 @@ int prepare_attention(AttnParams& p, const char* who, const void* q, int64_t qsb
     p.heads_magic = (uint32_t)((((uint64_t)1 << 32) + (uint64_t)heads - 1) / (uint64_t)heads);
   }
   p.scale_log2 = scale * kLog2e;
+  p.part = nullptr;
+  return SKV_OK;
+}
+
+// The split-K partials of a launch whose rows span nchunk_max > 1 chunks go to the
+// caller's workspace: check that it holds them and bind it.
+int bind_workspace(AttnParams& p, const char* who, int32_t d, void* ws, int64_t ws_bytes) {
+  const int64_t need = workspace_bytes((int64_t)p.batch * p.qlen, p.heads, d, p.nchunk_max);
+  if (need > 0 && (!ws || ws_bytes < need || !aligned16(ws)))
+    return fail(SKV_EWORKSPACE, "%s: workspace needs %lld bytes (16-byte aligned), got %lld", who, (long long)need,
+                (long long)ws_bytes);
   p.part = need > 0 ? (float*)ws : nullptr;
   return SKV_OK;
 }
@@ -2541,51 +2569,60 @@ int32_t skv_default_chunk_tokens(int32_t rows, int32_t num_heads, int32_t head_d
   return pick_chunk(rows, num_heads, head_dim, max_len, dtype);
 }
 
-int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
-                        void* k_pool, void* v_pool, const int32_t* block_tables, int32_t table_stride,
-                        const int32_t* table_rows, const int32_t* ctx_lens, const void* k_new, const void* v_new,
-                        int64_t new_stride_b, int64_t new_stride_q, int64_t new_stride_h, void* out,
-                        int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h, int32_t batch, int32_t q_len,
-                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                        int32_t num_blocks, int32_t max_ctx, float scale, int32_t causal, int32_t dtype,
-                        int32_t chunk_tokens, void* workspace, int64_t workspace_bytes, void* stream) {
+int32_t skv_paged_chunk_tokens(int32_t rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t max_ctx, int32_t dtype, int32_t block_size, int32_t num_blocks) {
+  return paged_chunk(rows, num_heads, num_kv_heads > 0 ? num_kv_heads : num_heads, head_dim, max_ctx, dtype,
+                     block_size, num_blocks);
+}
+
+}  // extern "C"
+
+namespace {
+
+// skv_paged_attention with a workspace (the caller's, or the library's
+// fixed scratch for the allocation-free entry point).
+int paged_attention_impl(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
+                         void* k_pool, void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                         const int32_t* table_rows, const int32_t* ctx_lens, const void* k_new, const void* v_new,
+                         int64_t new_stride_b, int64_t new_stride_q, int64_t new_stride_h, void* out,
+                         int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h, int32_t batch, int32_t q_len,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                         int32_t num_blocks, int32_t max_ctx, float scale, int32_t causal, int32_t dtype,
+                         int32_t chunk_tokens, void* workspace, int64_t ws_bytes, bool fixed_scratch,
+                         void* stream) {
   if (block_size < 2 || num_blocks < 0 || table_stride <= 0 || !block_tables)
-    return fail(SKV_EINVAL, "skv_paged_attention: bad block table arguments (block_size must be >= 2)");
+    return fail(SKV_EINVAL, "%s: bad block table arguments (block_size must be >= 2)", who);
   if ((k_new == nullptr) != (v_new == nullptr))
-    return fail(SKV_EINVAL, "skv_paged_attention: k_new and v_new must both be given or both be NULL");
+    return fail(SKV_EINVAL, "%s: k_new and v_new must both be given or both be NULL", who);
   const int64_t table_cap = (int64_t)table_stride * block_size;
   if (max_ctx > table_cap) max_ctx = (int32_t)table_cap;
-  AttnParams p{};
-  int rc = prepare_attention(p, "skv_paged_attention", q, q_stride_b, q_stride_q, q_stride_h, k_pool, v_pool, out,
-                             o_stride_b, o_stride_q, o_stride_h, ctx_lens, batch, q_len, num_heads, num_kv_heads,
-                             head_dim, max_ctx, scale, causal, dtype, chunk_tokens, workspace, workspace_bytes);
-  if (rc != SKV_OK) return rc;
   // The general paged path (a block size that is not a power of two of at least one load
   // instruction's keys, or a pool past the 32-bit buffer range) stages a chunk's block ids in
-  // kMaxChunkBlocks LDS slots; the fast path and the multi-query kernels read block ids with
-  // scalar loads and take chunks of any length.
-  {
-    const int epl = 16 / elt_bytes(dtype);
-    const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz((unsigned)block_size) : -1;
-    const int64_t kv_bytes = (int64_t)num_blocks * block_size * ((int64_t)num_kv_heads * head_dim / epl) * 16;
-    const bool fast = kv_bytes <= kBufLimit && bs_shift >= 0 && (1 << bs_shift) >= 64 * epl / head_dim;
-    if (!fast && p.chunk / block_size + 2 > kMaxChunkBlocks)
-      return fail(SKV_EINVAL,
-                  "skv_paged_attention: chunk_tokens %d spans more than %d blocks of %d (pass a smaller chunk_tokens)",
-                  p.chunk, kMaxChunkBlocks - 2, block_size);
-  }
+  // kMaxChunkBlocks LDS slots, so its default chunk stays within that many blocks; the fast
+  // path and the multi-query kernels read block ids with scalar loads and take chunks of any
+  // length.
+  const bool fast = elt_bytes(dtype) != 0 && paged_fast(dtype, head_dim, num_kv_heads, block_size, num_blocks);
+  if (chunk_tokens <= 0 && elt_bytes(dtype) != 0 && num_kv_heads > 0 && supported_d(head_dim))
+    chunk_tokens = paged_chunk(batch * q_len, num_heads, num_kv_heads, head_dim, max_ctx > 0 ? max_ctx : 1, dtype,
+                               block_size, num_blocks);
+  AttnParams p{};
+  int rc = prepare_attention(p, who, q, q_stride_b, q_stride_q, q_stride_h, k_pool, v_pool, out, o_stride_b,
+                             o_stride_q, o_stride_h, ctx_lens, batch, q_len, num_heads, num_kv_heads, head_dim,
+                             max_ctx, scale, causal, dtype, chunk_tokens);
+  if (rc != SKV_OK) return rc;
+  if (!fast && p.chunk / block_size + 2 > kMaxChunkBlocks)
+    return fail(SKV_EINVAL, "%s: chunk_tokens %d spans more than %d blocks of %d (pass a smaller chunk_tokens)", who,
+                p.chunk, kMaxChunkBlocks - 2, block_size);
   if (k_new) {
     const int epl = 16 / elt_bytes(dtype);
     if (!aligned16(k_new) || !aligned16(v_new) || new_stride_b % epl || new_stride_q % epl || new_stride_h % epl)
-      return fail(SKV_EALIGN, "skv_paged_attention: k_new/v_new must be 16-byte aligned with strides in %d-element units",
-                  epl);
+      return fail(SKV_EALIGN, "%s: k_new/v_new must be 16-byte aligned with strides in %d-element units", who, epl);
     p.kn = (const uint4*)k_new;
     p.vn = (const uint4*)v_new;
     p.nsb = new_stride_b / epl;
     p.nsq = new_stride_q / epl;
     p.nsh = new_stride_h / epl;
   }
-  if (batch == 0) return SKV_OK;
   p.tables = block_tables;
   p.tstride = table_stride;
   p.trows = table_rows;
@@ -2595,18 +2632,54 @@ int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   p.row_vecs = (int64_t)num_kv_heads * head_dim / (16 / elt_bytes(dtype));
   p.kv_bytes = (int64_t)num_blocks * block_size * p.row_vecs * 16;
   // Several non-causal queries per row with no fused append (attention over a whole encoder
-  // table, EncoderAttentionBackend): every 16 queries of a row share one read of its blocks.
-  if (!p.causal && q_len >= 2 && !k_new && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
-      p.kv_bytes <= kBufLimit && p.bs_shift >= 3 && batch <= 65535) {
-    if (use_mqt(p))
+  // table, EncoderAttentionBackend): every 16 queries of a row share one read of its blocks;
+  // the 64-query kernel takes all of a row's keys in one workgroup, so it needs no partials.
+  const bool mq = !p.causal && q_len >= 2 && !k_new && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
+                  p.kv_bytes <= kBufLimit && p.bs_shift >= 3 && batch <= 65535;
+  const bool mqt = mq && use_mqt(p);
+  if (mqt) {
+    p.nchunk_max = 1;
+    p.snake = 0;
+  }
+  rc = bind_workspace(p, who, head_dim, workspace, ws_bytes);
+  if (rc != SKV_OK) {
+    if (!fixed_scratch) return rc;
+    return fail(SKV_EWORKSPACE,
+                "%s: this call needs %lld bytes of split-K partials, more than the %lld bytes of the library's fixed "
+                "scratch; use skv_paged_attention with a workspace, or larger chunk_tokens", who,
+                (long long)workspace_bytes((int64_t)batch * q_len, num_heads, head_dim, p.nchunk_max),
+                (long long)ws_bytes);
+  }
+  if (batch == 0) return SKV_OK;
+  if (mq) {
+    if (mqt)
       launch_mqt<true>(dtype, p, (hipStream_t)stream);
     else
       launch_mq<true>(dtype, p, (hipStream_t)stream);
-    return check_launch("skv_paged_attention");
+    return check_launch(who);
   }
   rc = dispatch_attention<true>(dtype, head_dim, p, (hipStream_t)stream);
   if (rc != SKV_OK) return rc;
-  return check_launch("skv_paged_attention");
+  return check_launch(who);
+}
+
+}  // namespace
+
+extern "C" {
+
+int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
+                        void* k_pool, void* v_pool, const int32_t* block_tables, int32_t table_stride,
+                        const int32_t* table_rows, const int32_t* ctx_lens, const void* k_new, const void* v_new,
+                        int64_t new_stride_b, int64_t new_stride_q, int64_t new_stride_h, void* out,
+                        int64_t o_stride_b, int64_t o_stride_q, int64_t o_stride_h, int32_t batch, int32_t q_len,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        int32_t num_blocks, int32_t max_ctx, float scale, int32_t causal, int32_t dtype,
+                        int32_t chunk_tokens, void* workspace, int64_t workspace_bytes, void* stream) {
+  return paged_attention_impl("skv_paged_attention", q, q_stride_b, q_stride_q, q_stride_h, k_pool, v_pool,
+                              block_tables, table_stride, table_rows, ctx_lens, k_new, v_new, new_stride_b,
+                              new_stride_q, new_stride_h, out, o_stride_b, o_stride_q, o_stride_h, batch, q_len,
+                              num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_ctx, scale, causal,
+                              dtype, chunk_tokens, workspace, workspace_bytes, false, stream);
 }
 
 int skv_paged_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,
@@ -2617,29 +2690,14 @@ int skv_paged_attention_noalloc(const void* q, int64_t q_stride_b, int64_t q_str
                                 int32_t q_len, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                 int32_t block_size, int32_t num_blocks, int32_t max_ctx, float scale, int32_t causal,
                                 int32_t dtype, int32_t chunk_tokens, void* stream) {
-  // The split-K partials this call needs, worked out as skv_paged_attention does (its own
-  // validation reports malformed arguments below).
-  if (batch > 0 && q_len > 0 && num_heads > 0 && block_size > 0 && table_stride > 0 && max_ctx > 0 &&
-      elt_bytes(dtype) != 0 && supported_d(head_dim)) {
-    const int64_t cap = (int64_t)table_stride * block_size;
-    const int32_t len = max_ctx > cap ? (int32_t)cap : max_ctx;
-    const int32_t chunk =
-        chunk_tokens > 0 ? chunk_tokens : pick_chunk(batch * q_len, num_heads, head_dim, len, dtype);
-    const int64_t need = workspace_bytes((int64_t)batch * q_len, num_heads, head_dim, cdiv(len, chunk));
-    if (need > kScratchBytes)
-      return fail(SKV_EWORKSPACE,
-                  "skv_paged_attention_noalloc: this call needs %lld bytes of split-K partials, more than the %lld "
-                  "bytes of the library's fixed scratch; use skv_paged_attention with a workspace, or larger "
-                  "chunk_tokens", (long long)need, (long long)kScratchBytes);
-  }
   void* ws = nullptr;
   const int rc = scratch_on_current_device(&ws);
   if (rc != SKV_OK) return rc;
-  return skv_paged_attention(q, q_stride_b, q_stride_q, q_stride_h, k_pool, v_pool, block_tables, table_stride,
-                             table_rows, ctx_lens, k_new, v_new, new_stride_b, new_stride_q, new_stride_h, out,
-                             o_stride_b, o_stride_q, o_stride_h, batch, q_len, num_heads, num_kv_heads, head_dim,
-                             block_size, num_blocks, max_ctx, scale, causal, dtype, chunk_tokens, ws, kScratchBytes,
-                             stream);
+  return paged_attention_impl("skv_paged_attention_noalloc", q, q_stride_b, q_stride_q, q_stride_h, k_pool, v_pool,
+                              block_tables, table_stride, table_rows, ctx_lens, k_new, v_new, new_stride_b,
+                              new_stride_q, new_stride_h, out, o_stride_b, o_stride_q, o_stride_h, batch, q_len,
+                              num_heads, num_kv_heads, head_dim, block_size, num_blocks, max_ctx, scale, causal,
+                              dtype, chunk_tokens, ws, kScratchBytes, true, stream);
 }
 
 int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h, const void* k,
@@ -2651,12 +2709,11 @@ int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   AttnParams p{};
   int rc = prepare_attention(p, "skv_dense_attention", q, q_stride_b, q_stride_q, q_stride_h, k, v, out, o_stride_b,
                              o_stride_q, o_stride_h, lens, batch, q_len, num_heads, num_kv_heads, head_dim, max_len,
-                             scale, causal, dtype, chunk_tokens, workspace, workspace_bytes);
+                             scale, causal, dtype, chunk_tokens);
   if (rc != SKV_OK) return rc;
   const int epl = 16 / elt_bytes(dtype);
   if (kv_stride_s % epl || kv_stride_h % epl || kv_stride_t % epl)
     return fail(SKV_EALIGN, "skv_dense_attention: K/V strides must be multiples of %d elements", epl);
-  if (batch == 0) return SKV_OK;
   p.ss = kv_stride_s / epl;
   p.sh = kv_stride_h / epl;
   p.st = kv_stride_t / epl;
@@ -2665,10 +2722,20 @@ int skv_dense_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, i
   if (p.st < 0) p.kv_bytes = kBufLimit + 1;  // negative key strides take the 64-bit path
   p.slots = slot_ids;
   // Several non-causal queries per row (a prompt's cross-attention): one workgroup per
-  // tile of 16 queries reads the row's K/V once and runs both products on the matrix cores.
-  if (!p.causal && q_len >= 2 && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
-      p.kv_bytes <= kBufLimit && p.st > 0 && batch <= 65535) {
-    if (use_mqt(p))
+  // tile of 16 queries reads the row's K/V once and runs both products on the matrix cores;
+  // the 64-query kernel takes all of a row's keys in one workgroup (no partials).
+  const bool mq = !p.causal && q_len >= 2 && head_dim == 64 && (dtype == SKV_F16 || dtype == SKV_BF16) &&
+                  p.kv_bytes <= kBufLimit && p.st > 0 && batch <= 65535;
+  const bool mqt = mq && use_mqt(p);
+  if (mqt) {
+    p.nchunk_max = 1;
+    p.snake = 0;
+  }
+  rc = bind_workspace(p, "skv_dense_attention", head_dim, workspace, workspace_bytes);
+  if (rc != SKV_OK) return rc;
+  if (batch == 0) return SKV_OK;
+  if (mq) {
+    if (mqt)
       launch_mqt<false>(dtype, p, (hipStream_t)stream);
     else
       launch_mq<false>(dtype, p, (hipStream_t)stream);

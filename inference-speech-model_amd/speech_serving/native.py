@@ -39,6 +39,7 @@ SIGNATURES = {
                                    _c_i32, _c_i32, _c_i32, _c_p]),
     "skv_attention_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "skv_default_chunk_tokens": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "skv_paged_chunk_tokens": (_c_i32, [_c_i32] * 8),
     "skv_paged_attention": (_c_int, [_c_p, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_p,
                                      _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_p,
                                      _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
@@ -208,6 +209,13 @@ def attention_workspace_bytes(rows: int, heads: int, head_dim: int, max_len: int
 
 def default_chunk_tokens(rows: int, heads: int, head_dim: int, max_len: int, dtype: torch.dtype) -> int:
     return int(lib().skv_default_chunk_tokens(rows, heads, head_dim, max_len, _code(dtype)))
+
+
+def paged_chunk_tokens(rows: int, heads: int, kv_heads: int, head_dim: int, max_ctx: int, dtype: torch.dtype,
+                       block_size: int, num_blocks: int) -> int:
+    """The chunk skv_paged_attention takes by default for pools of num_blocks x block_size tokens."""
+    return int(lib().skv_paged_chunk_tokens(rows, heads, kv_heads, head_dim, max_ctx, _code(dtype), block_size,
+                                            num_blocks))
 
 
 # ---------------------------------------------------------------------------
@@ -458,7 +466,7 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     code = _code(q4.dtype)
     max_ctx = max(0, min(int(max_ctx), block_tables.shape[1] * bs))
     if chunk_tokens <= 0:
-        chunk_tokens = default_chunk_tokens(bsz * qlen, heads, d, max(max_ctx, 1), q4.dtype)
+        chunk_tokens = paged_chunk_tokens(bsz * qlen, heads, hkv, d, max(max_ctx, 1), q4.dtype, bs, nb)
     kn4 = vn4 = None
     nstr = (0, 0, 0)
     if (k_new is None) != (v_new is None):

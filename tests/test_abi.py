@@ -71,6 +71,29 @@ def test_default_chunk():
     assert lib.skv_default_chunk_tokens(1, 1, 64, 10, native.SKV_F32) == 128
 
 
+def test_paged_default_chunk_fits_staged_block_ids():
+    """Pools read through staged block ids (block sizes that are not powers of two, blocks shorter
+    than one load instruction's keys, pools past 2 GiB) keep the default chunk within 254 blocks
+    and a whole number of 64-key sub-chunks; the fast path keeps the dense default."""
+    lib = native.lib()
+    bf16 = native.SKV_BF16
+    # 8 rows x 20 heads over 1500 keys: one 1536-key chunk by default; block size 6 caps it.
+    assert lib.skv_paged_chunk_tokens(8, 20, 20, 64, 1500, bf16, 16, 4096) == 1536
+    c = lib.skv_paged_chunk_tokens(8, 20, 20, 64, 1500, bf16, 6, 4096)
+    assert c == (254 * 6 // 64) * 64 == 1472
+    assert c // 6 + 2 <= 256
+    # 64 rows x 16 heads over 4100 keys: block size 12 -> at most 254 * 12 = 3048 keys.
+    assert lib.skv_paged_chunk_tokens(64, 16, 16, 64, 4100, bf16, 16, 20000) == 4352
+    assert lib.skv_paged_chunk_tokens(64, 16, 16, 64, 4100, bf16, 12, 20000) == (254 * 12 // 64) * 64
+    # 4-token blocks are below one bf16 D=64 load instruction's 8 keys: general path.
+    assert lib.skv_paged_chunk_tokens(64, 16, 16, 64, 4100, bf16, 4, 80000) == (254 * 4 // 64) * 64
+    # A 16-token-block pool past 2 GiB per layer (70000 blocks x 16 x 16 heads x 128 B) is general too.
+    assert lib.skv_paged_chunk_tokens(64, 16, 16, 64, 4100, bf16, 16, 70000) == (254 * 16 // 64) * 64
+    # Short rows are unaffected by the cap.
+    assert lib.skv_paged_chunk_tokens(64, 20, 20, 64, 448, bf16, 6, 4096) == \
+        lib.skv_default_chunk_tokens(64, 20, 64, 448, bf16)
+
+
 FAKE = 1 << 20  # aligned, never dereferenced: validation fails before any launch
 
 

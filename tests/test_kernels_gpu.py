@@ -172,17 +172,23 @@ def test_paged_attention_few_rows_long_context_default_split(cuda, dtype, bs):
 
 
 # ------------------------------------------------------------------ paged attention
-@pytest.mark.parametrize("bs,max_ctx", [(16, 4100), (8, 2100), (12, 4100)])
-def test_paged_attention_long_context_default_chunk(cuda, bs, max_ctx):
-    """1024 (row, head) pairs take one chunk per row by default; at these contexts that chunk spans more
-    than the general path's 254 staged block ids. Power-of-two blocks (the fast path, block ids read per
-    trip) attend over it; a block size of 12 (the general path) reports the limit instead."""
+@pytest.mark.parametrize("bsz,h,bs,max_ctx", [(64, 16, 16, 4100), (64, 16, 8, 2100), (64, 16, 12, 4100),
+                                               (8, 20, 6, 1500)])
+def test_paged_attention_long_context_default_chunk(cuda, bsz, h, bs, max_ctx):
+    """Rows whose default chunk would span more than the general path's 254 staged block ids. Power-of-two
+    blocks (the fast path, block ids read per trip) take one chunk per row; block sizes of 12 and 6 (the
+    general path) get the default chunk capped at 254 blocks (rows split, partials merged)."""
     gen = torch.Generator().manual_seed(bs + max_ctx)
-    bsz, h, d, dtype = 64, 16, 64, torch.bfloat16
+    d, dtype = 64, torch.bfloat16
     lens = [max_ctx, (max_ctx * 3) // 4] + torch.randint(1, 41, (bsz - 2,), generator=gen).tolist()
     maxblk = -(-max_ctx // bs)
     need = [-(-n // bs) for n in lens]
     nb = sum(need) + 8
+    chunk = native.paged_chunk_tokens(bsz, h, h, d, max_ctx, dtype, bs, nb)
+    if bs & (bs - 1):
+        assert chunk // bs + 2 <= 256 and chunk < max_ctx, chunk
+    else:
+        assert chunk == native.default_chunk_tokens(bsz, h, d, max_ctx, dtype), chunk
     kp, vp = make_pool(gen, nb, bs, h, d, dtype, cuda)
     perm = torch.randperm(nb, generator=gen).to(torch.int32)
     tables = torch.full((bsz, maxblk), -1, dtype=torch.int32)
@@ -191,16 +197,12 @@ def test_paged_attention_long_context_default_chunk(cuda, bs, max_ctx):
         tables[i, :n] = perm[at:at + n]
         at += n
     q = torch.randn(bsz, h, d, generator=gen).to(cuda, dtype)
-    call = lambda: native.paged_attention(q, kp, vp, tables.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
-                                          max_ctx, 0.125)
-    if bs & (bs - 1):
-        with pytest.raises(RuntimeError, match="chunk_tokens"):
-            call()
-        return
-    out = call()
+    out = native.paged_attention(q, kp, vp, tables.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda),
+                                 max_ctx, 0.125)
     torch.cuda.synchronize()
     want = O.paged_attention(f64(q)[:, None], f64(kp), f64(vp), tables.numpy(), lens, 0.125)[:, 0]
-    assert_close(out, want, dtype, f"long context bs={bs} max_ctx={max_ctx}")
+    err = assert_close(out, want, dtype, f"long context bs={bs} max_ctx={max_ctx}")
+    print(f"long context, default chunk {chunk}, block size {bs}: max err {err:.2e}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

@@ -41,6 +41,36 @@ def run(p, cuda, noalloc):
     return out, kp, vp
 
 
+def test_noalloc_graph_replays_equal_eager_calls(cuda):
+    """A split-K call captured into a HIP graph (run alone, this file makes the device's first
+    allocation-free call inside the capture, where the scratch address is looked up): replays with new
+    queries, with eager work and a sync between them, are bit-equal to eager calls of both entry points."""
+    dtype = torch.bfloat16
+    p = problem(cuda, dtype, 4, 8, 64, 16, 512, 1500, 5, fused=False)
+    assert native.attention_workspace_bytes(4, 8, 64, p["max_ctx"], dtype) > 0  # split-K is exercised
+    tables, ctx = p["tables"].to(cuda), p["ctx"].to(torch.int32).to(cuda)
+    scale = 1.0 / 8.0
+    q_static = p["q"].clone()
+    out_static = torch.empty_like(q_static)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        native.paged_attention(q_static, p["kp"], p["vp"], tables, ctx, p["max_ctx"], scale, out=out_static,
+                               noalloc=True)
+    gen = torch.Generator().manual_seed(6)
+    for i in range(4):
+        q_new = torch.randn(q_static.shape, generator=gen).to(cuda, dtype)
+        q_static.copy_(q_new)
+        g.replay()
+        torch.cuda.synchronize()
+        got = out_static.clone()
+        eager_noalloc = native.paged_attention(q_new, p["kp"], p["vp"], tables, ctx, p["max_ctx"], scale,
+                                               noalloc=True)
+        eager_ws = native.paged_attention(q_new, p["kp"], p["vp"], tables, ctx, p["max_ctx"], scale)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager_noalloc), f"replay {i}"
+        assert torch.equal(got, eager_ws), f"replay {i}"
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_noalloc_matches_the_workspace_entry_point_twice(cuda, dtype):
     # A few (row, head) pairs over long contexts: the keys split into chunks, so the partials go
@@ -60,6 +90,26 @@ def test_noalloc_matches_the_workspace_entry_point_twice(cuda, dtype):
         half_ulp = 2.0 ** -11 if dtype == torch.float16 else 2.0 ** -8
         err = np.abs(got_out.double().cpu().numpy() - ref)
         assert (err <= 2e-3 + half_ulp * np.abs(ref)).all(), float(err.max())
+
+
+def test_noalloc_encoder_attention_needs_no_scratch(cuda):
+    """Encoder attention over a paged table (1500 queries x 8 heads) takes the 64-query kernel, which
+    keeps each row's keys in one workgroup: no partials, so the call is accepted even with a chunk size
+    whose split-K partials would exceed the scratch, and it equals the workspace entry point."""
+    g = torch.Generator().manual_seed(9)
+    dtype, heads, d, bs, t = torch.bfloat16, 8, 64, 16, 1500
+    nblk = -(-t // bs)
+    kp = torch.randn(nblk + 4, bs, heads, d, generator=g).to(cuda, dtype)
+    vp = torch.randn(nblk + 4, bs, heads, d, generator=g).to(cuda, dtype)
+    tables = torch.randperm(nblk + 4, generator=g)[:nblk].view(1, nblk).to(torch.int32).to(cuda)
+    q = torch.randn(1, t, heads, d, generator=g).to(cuda, dtype)
+    lens = torch.tensor([t], dtype=torch.int32, device=cuda)
+    # chunk 64: 1500 query rows x 8 heads x 24 chunks of (64 + 4) floats = 78 MB of partials, were they used
+    assert native.attention_workspace_bytes(t, heads, d, t, dtype, 64) > (4 << 20)
+    got = native.paged_attention(q, kp, vp, tables, lens, t, 0.125, chunk_tokens=64, noalloc=True)
+    want = native.paged_attention(q, kp, vp, tables, lens, t, 0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
 
 
 def test_noalloc_refuses_partials_beyond_its_scratch(cuda):
