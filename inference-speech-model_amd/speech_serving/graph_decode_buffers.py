@@ -94,6 +94,11 @@ class GraphDecodeBuffers:
         block_manager: Optional[BlockManager] = None,
         capture: bool = True,
     ):
+        if not callable(getattr(model, "decode_step_paged", None)):
+            raise TypeError(
+                f"GraphDecodeBuffers captures the model's paged decode step (decode_step_paged); "
+                f"{type(model).__name__} exposes only decode_step, so serve it with graph_decode=False "
+                "(the scheduler then runs it eagerly on K/V gathered from the pool)")
         self.model = model
         self.device = torch.device(device)
         self.dtype = dtype

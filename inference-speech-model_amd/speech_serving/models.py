@@ -15,11 +15,16 @@ then the MLP normalises with norm3 (else norm2); no positional embedding.
 
 Entry points:
     encode(mel) -> (hidden, [(K, V)] per encoder layer)        models.py:349-367
-    decode_step(...)  contiguous past KV, reference signature   models.py:369-423
+    decode_step(...)  the reference signature                   models.py:369-423
+        With a PagedKVCache as past_key_values it runs the paged hot path (the
+        scheduler's eager prefill and decode call it so); any other cache (a
+        DynamicCache-like object with .layers, a list of (K, V), None) is
+        contiguous past K/V, as in the reference.
     decode_step_graph_fixed(...) bucketed static KV signature   models.py:425-487
-    decode_step_paged(ids, PagedKV, CrossKV)  the paged hot path: per layer one
-        fused launch appends the new K/V through the block table and attends,
-        and one launch attends the slot's contiguous encoder K/V.
+    decode_step_paged(ids, PagedKV, CrossKV)  the paged step itself: per layer
+        one fused launch appends the new K/V through the block table and
+        attends, and one launch attends the rows' contiguous encoder K/V (the
+        captured graph decode step calls it directly).
     project_cross_kv(hidden) -> [(K, V)] per decoder layer via cross_attn_k/v.
 Every attention, append and greedy step is a HIP kernel (speech_serving.native);
 tensors must live on the GPU.
@@ -83,6 +88,65 @@ class PagedKV:
     ctx_lens: torch.Tensor
     max_ctx: int
     table_rows: Optional[torch.Tensor] = None
+
+
+class _GatheredLayer:
+    """One layer of a PagedKVCache as contiguous [B, H, max_ctx, D] K/V (zero past each row's length)."""
+
+    def __init__(self, cache: "PagedKVCache", layer: int):
+        self._cache, self._layer = cache, layer
+        self._kv: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+        self.is_initialized = True
+
+    def _get(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        if self._kv is None:
+            c = self._cache
+            tables = c.block_tables if c.table_rows is None else c.block_tables.index_select(0, c.table_rows.long())
+            self._kv = native.gather(c.k_pools[self._layer], c.v_pools[self._layer], tables,
+                                     c.ctx_lens[: c.batch], c.max_ctx)
+        return self._kv
+
+    @property
+    def keys(self) -> torch.Tensor:
+        return self._get()[0]
+
+    @property
+    def values(self) -> torch.Tensor:
+        return self._get()[1]
+
+
+class PagedKVCache:
+    """Self-attention K/V of a decode batch held in a BlockManager pool, passed to
+    decode_step as `past_key_values` (where the reference passes a DynamicCache of
+    contiguous K/V, phase_aware_scheduler.py:793-846 and :982-991).
+
+    It describes the cache as it stands once the call's tokens are in: row b's block
+    table (table row table_rows[b], or b) covers ctx_lens[b] keys, the last Q of which
+    are the Q tokens of input_ids (positions ctx_lens[b]-Q .. ctx_lens[b]-1). decode_step
+    appends their K/V through the tables inside the attention launch and returns this
+    object as its output's past_key_values. `.layers[l].keys / .values` gather layer l
+    into a zero-padded [B, H, max_ctx, D] batch (skv_gather) for code that reads a cache
+    the way the reference reads its DynamicCache.
+
+    cross_lens / cross_mask: the batch's encoder lengths (int32 [B] on the device) and the
+    encoder_attention_mask built from them. decode_step takes the lengths as they are when
+    it receives that same mask object, and derives them from any other mask."""
+
+    def __init__(self, k_pools: Sequence[torch.Tensor], v_pools: Sequence[torch.Tensor], block_tables: torch.Tensor,
+                 ctx_lens: torch.Tensor, max_ctx: int, table_rows: Optional[torch.Tensor] = None,
+                 cross_lens: Optional[torch.Tensor] = None, cross_mask: Optional[torch.Tensor] = None):
+        self.k_pools, self.v_pools = k_pools, v_pools
+        self.block_tables, self.ctx_lens, self.max_ctx = block_tables, ctx_lens, int(max_ctx)
+        self.table_rows = table_rows
+        self.cross_lens, self.cross_mask = cross_lens, cross_mask
+        self.batch = int(ctx_lens.shape[0])
+        self.layers = [_GatheredLayer(self, l) for l in range(len(k_pools))]
+
+    def __len__(self) -> int:
+        return len(self.layers)
+
+    def paged(self) -> "PagedKV":
+        return PagedKV(self.k_pools, self.v_pools, self.block_tables, self.ctx_lens, self.max_ctx, self.table_rows)
 
 
 @dataclass
@@ -416,13 +480,25 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
         _, h = add_norm(x, pending, self.decoder_norm)
         return self.lm_head(h)
 
-    # -- contiguous decode, reference signature (models.py:369-423) --------------------
+    # -- decode step, reference signature (models.py:369-423) ----------------------------
     def decode_step(self, input_ids: torch.Tensor, past_key_values: Optional[Any] = None,
                     encoder_past_kv_list: Optional[List[Tuple[torch.Tensor, torch.Tensor]]] = None,
                     encoder_hidden_states: Optional[torch.Tensor] = None,
                     attention_mask: Optional[torch.Tensor] = None,
                     encoder_attention_mask: Optional[torch.Tensor] = None,
                     position_ids: Optional[torch.Tensor] = None, use_cache: bool = True, **kwargs) -> ModelOutput:
+        """Logits [B, S, V] of input_ids [B, S] and the updated cache.
+
+        past_key_values: a PagedKVCache (the paged hot path), or contiguous past K/V as in the
+        reference (an object with .layers[l].keys/.values, a list of (K, V) [B, H, T, D], or None).
+        encoder_past_kv_list: per decoder layer (K, V) [B or 1, H, T_enc, D], row b of the batch
+        attending row b; layers past the list's end use encoder_hidden_states (projected) or no
+        cross-attention. Masks as in the reference (models.py:142-157, 186-199).
+        logits_to_keep (keyword): when > 0, logits of the last logits_to_keep positions only."""
+        if isinstance(past_key_values, PagedKVCache):
+            return self._decode_step_paged_cache(input_ids, past_key_values, encoder_past_kv_list,
+                                                 encoder_hidden_states, attention_mask, encoder_attention_mask,
+                                                 int(kwargs.get("logits_to_keep", 0) or 0))
         x = self._embed(input_ids)
         cache = KVCache() if use_cache else None
         for i, layer in enumerate(self.decoder_layers):
@@ -441,7 +517,74 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
                                  encoder_attention_mask=encoder_attention_mask)
             if use_cache:
                 cache.layers.append(LayerKV(new_kv[0], new_kv[1]))
+        keep = int(kwargs.get("logits_to_keep", 0) or 0)
+        if keep > 0:
+            x = x[:, -keep:]
         return ModelOutput(self.lm_head(self.decoder_norm(x)), cache)
+
+    def _decode_step_paged_cache(self, input_ids: torch.Tensor, cache: PagedKVCache,
+                                 encoder_past_kv_list: Optional[List[Tuple[torch.Tensor, torch.Tensor]]],
+                                 encoder_hidden_states: Optional[torch.Tensor],
+                                 attention_mask: Optional[torch.Tensor],
+                                 encoder_attention_mask: Optional[torch.Tensor], keep: int) -> ModelOutput:
+        b = input_ids.shape[0]
+        if attention_mask is not None:
+            raise ValueError("decode_step: a PagedKVCache carries each row's length; attention_mask must be None")
+        if cache.batch < b:
+            raise ValueError(f"decode_step: the PagedKVCache holds {cache.batch} rows for a batch of {b}")
+        cross = self._cross_kv(b, encoder_past_kv_list, encoder_hidden_states, encoder_attention_mask, cache)
+        if keep == 1:
+            logits = self.decode_step_paged(input_ids, cache.paged(), cross, last_only=True).unsqueeze(1)
+        else:
+            logits = self.decode_step_paged(input_ids, cache.paged(), cross, last_only=False)
+            if keep > 1:
+                logits = logits[:, -keep:]
+        return ModelOutput(logits, cache)
+
+    def _cross_kv(self, b: int, enc_list: Optional[List[Tuple[torch.Tensor, torch.Tensor]]],
+                  enc_hidden: Optional[torch.Tensor], enc_mask: Optional[torch.Tensor],
+                  cache: PagedKVCache) -> Optional[CrossKV]:
+        """The decode_step's encoder inputs as per-layer [B, H, T, D] K/V and per-row lengths: the given
+        (K, V) per layer, then (for the layers past the list) K/V projected from encoder_hidden_states
+        (models.py:179-181, 398-406)."""
+        n = self.num_decoder_layers
+        ks: List[torch.Tensor] = []
+        vs: List[torch.Tensor] = []
+        dt = self.dtype
+        for k, v in (enc_list or [])[:n]:
+            if k.dim() != 4 or k.shape[1] != self.num_heads or k.shape[3] != self.head_dim or \
+                    k.shape[0] not in (1, b) or v.shape != k.shape:
+                raise ValueError(f"decode_step: encoder K/V must be [{b} or 1, {self.num_heads}, T, "
+                                 f"{self.head_dim}], got {tuple(k.shape)} / {tuple(v.shape)}")
+            k, v = k.to(dt), v.to(dt)
+            if k.stride(3) != 1 or k.stride() != v.stride():
+                k, v = k.contiguous(), v.contiguous()
+            if k.shape[0] == 1 and b > 1:
+                k, v = k.expand(b, -1, -1, -1), v.expand(b, -1, -1, -1)
+            ks.append(k)
+            vs.append(v)
+        if enc_hidden is not None and len(ks) < n:
+            h = enc_hidden.to(dt)
+            te = h.shape[1]
+            for layer in self.decoder_layers[len(ks):]:
+                ks.append(layer.cross_attn_k(h).view(h.shape[0], te, self.num_heads, self.head_dim)
+                          .transpose(1, 2).contiguous().expand(b, -1, -1, -1))
+                vs.append(layer.cross_attn_v(h).view(h.shape[0], te, self.num_heads, self.head_dim)
+                          .transpose(1, 2).contiguous().expand(b, -1, -1, -1))
+        if not ks:
+            return None
+        t = ks[0].shape[2]
+        if any(k.shape[2] != t for k in ks):
+            raise ValueError("decode_step: every layer's encoder K/V must cover the same positions")
+        if enc_mask is None:
+            lens = torch.full((b,), t, dtype=torch.int32, device=ks[0].device)
+        elif enc_mask is cache.cross_mask and cache.cross_lens is not None:
+            lens = cache.cross_lens[:b]
+        else:
+            keep = _keep_mask(enc_mask, b, t)
+            for i in range(len(ks)):
+                ks[i], vs[i], lens = _compact(ks[i], vs[i], keep)
+        return CrossKV(ks, vs, lens, t)
 
     # -- bucketed static-KV decode, reference signature (models.py:425-487) -------------
     def decode_step_graph_fixed(self, g_token_ids: torch.Tensor, g_positions: torch.Tensor, g_self_kv: torch.Tensor,
@@ -577,7 +720,17 @@ class StreamingMultiCodebookTTSModel(nn.Module):
         return self.norm.weight.dtype
 
     def forward(self, input_codebooks: torch.Tensor, past_key_values: Optional[Any] = None,
-                use_cache: bool = True) -> ModelOutput:
+                use_cache: bool = True, logits_to_keep: int = 0) -> ModelOutput:
+        """Logits [B, S, K, V] of input_codebooks [B, S, K] and the updated cache. With a PagedKVCache as
+        past_key_values this is the paged step (the frames' K/V go into the pool through the block
+        tables); otherwise past K/V are contiguous, as in the reference. logits_to_keep > 0 keeps the
+        logits of the last logits_to_keep frames only."""
+        if isinstance(past_key_values, PagedKVCache):
+            if logits_to_keep == 1:
+                logits = self.decode_step_paged(input_codebooks, past_key_values.paged(), last_only=True)
+                return ModelOutput(logits.unsqueeze(1), past_key_values)
+            logits = self.decode_step_paged(input_codebooks, past_key_values.paged(), last_only=False)
+            return ModelOutput(logits[:, -logits_to_keep:] if logits_to_keep > 0 else logits, past_key_values)
         x = self.embeddings(input_codebooks)
         cache = KVCache() if use_cache else None
         for i, layer in enumerate(self.layers):
@@ -591,6 +744,8 @@ class StreamingMultiCodebookTTSModel(nn.Module):
             x, new_kv, _ = layer(x, past_key_values=past)
             if use_cache:
                 cache.layers.append(LayerKV(new_kv[0], new_kv[1]))
+        if logits_to_keep > 0:
+            x = x[:, -logits_to_keep:]
         return ModelOutput(self.heads(self.norm(x)), cache)
 
     def decode_step_paged(self, input_codebooks: torch.Tensor, kv: PagedKV, last_only: bool = True) -> torch.Tensor:

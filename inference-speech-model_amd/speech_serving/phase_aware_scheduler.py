@@ -33,7 +33,7 @@ from . import native
 from .dual_cache_manager import DualCacheManager
 from .graph_decode_buffers import MAX_SLOTS, DEFAULT_READBACK_K, GraphDecodeBuffers
 from .memory_guard import MemoryGuard, logger
-from .models import CrossKV, PagedKV
+from .models import KVCache, LayerKV, PagedKVCache
 from .phase_timing import PhaseTimer
 
 WHISPER_SOT_TOKEN_ID = 50258
@@ -92,18 +92,22 @@ class DualCacheRequest:
 
 
 class CrossArena:
-    """Slot-major encoder K/V for eager decode: [S, L, 2, H, T, D] with a free list.
+    """Slot-major encoder K/V for eager decode: [S, L, 2, H, T, D].
 
-    T grows (reallocate + copy of the live slots) when a request needs more
-    encoder positions than the arena holds.
+    The live requests hold slots 0..n-1: a released slot is refilled by moving the last live
+    slot into it. A batch laid out in slot order therefore reads its encoder K/V as the
+    per-layer views buf[lo:hi, l, 0|1, :, :T], the [B, H, T, D] tensors that decode_step
+    takes as encoder_past_kv_list (the reference batches each step's encoder K/V into such
+    tensors, phase_aware_scheduler.py:848-970). T grows (reallocate + copy of the live
+    slots) when a request needs more encoder positions than the arena holds.
     """
 
     def __init__(self, slots: int, layers: int, heads: int, head_dim: int, dtype, device):
         self.slots, self.layers, self.heads, self.head_dim = slots, layers, heads, head_dim
         self.dtype, self.device = dtype, device
         self.buf: Optional[torch.Tensor] = None
-        self.free = list(range(slots - 1, -1, -1))
-        self.live: Dict[int, int] = {}
+        self.owner: List[Any] = []  # owner[s]: the request in slot s
+        self.lens: List[int] = []  # encoder positions held in slot s
 
     @property
     def max_len(self) -> int:
@@ -116,29 +120,32 @@ class CrossArena:
         new = torch.zeros((self.slots, self.layers, 2, self.heads, new_t, self.head_dim), dtype=self.dtype,
                           device=self.device)
         if self.buf is not None:
-            for s, n in self.live.items():
+            for s, n in enumerate(self.lens):
                 new[s, :, :, :, :n].copy_(self.buf[s, :, :, :, :n])
         self.buf = new
 
-    def put(self, enc_kv: List[Tuple[torch.Tensor, torch.Tensor]]) -> Tuple[int, int]:
-        """Copy one request's per-layer K/V [1, H, T, D] into a free slot; returns (slot, T)."""
-        if not self.free:
+    def _take(self, req, t: int) -> int:
+        if len(self.owner) >= self.slots:
             raise RuntimeError("cross-attention arena is full")
-        t = enc_kv[0][0].shape[2]
         self._ensure(t)
-        s = self.free.pop()
+        s = len(self.owner)
+        self.owner.append(req)
+        self.lens.append(t)
+        req.cross_slot = s
+        return s
+
+    def put(self, req, enc_kv: List[Tuple[torch.Tensor, torch.Tensor]]) -> int:
+        """Copy one request's per-layer K/V [1, H, T, D] into the next slot; returns the slot."""
+        t = enc_kv[0][0].shape[2]
+        s = self._take(req, t)
         for l, (k, v) in enumerate(enc_kv[: self.layers]):
             self.buf[s, l, 0, :, :t].copy_(k[0])
             self.buf[s, l, 1, :, :t].copy_(v[0])
-        self.live[s] = t
-        return s, t
+        return s
 
-    def put_from_pool(self, enc_bm, block_table: List[int], t: int, layers: int) -> Tuple[int, int]:
-        """Gather a request's encoder K/V from the encoder pool straight into a free slot."""
-        if not self.free:
-            raise RuntimeError("cross-attention arena is full")
-        self._ensure(t)
-        s = self.free.pop()
+    def put_from_pool(self, req, enc_bm, block_table: List[int], t: int, layers: int) -> int:
+        """Gather a request's encoder K/V from the encoder pool straight into the next slot."""
+        s = self._take(req, t)
         dev = self.buf.device
         tbl = torch.tensor([block_table], dtype=torch.int32, device=dev)
         lens = torch.tensor([t], dtype=torch.int32, device=dev)
@@ -146,13 +153,36 @@ class CrossArena:
         for l in range(min(layers, self.layers)):
             native.gather(enc_bm.key_pool[l], enc_bm.value_pool[l], tbl, lens, tmax,
                           k_out=self.buf[s, l, 0].unsqueeze(0), v_out=self.buf[s, l, 1].unsqueeze(0))
-        self.live[s] = t
-        return s, t
+        return s
 
-    def release(self, s: int) -> None:
-        if s in self.live:
-            del self.live[s]
-            self.free.append(s)
+    def release(self, req) -> None:
+        s = getattr(req, "cross_slot", None)
+        if s is None or s >= len(self.owner) or self.owner[s] is not req:
+            return
+        last = len(self.owner) - 1
+        if s != last:
+            n = self.lens[last]
+            self.buf[s, :, :, :, :n].copy_(self.buf[last, :, :, :, :n])
+            self.owner[s], self.lens[s] = self.owner[last], n
+            self.owner[s].cross_slot = s
+        self.owner.pop()
+        self.lens.pop()
+        req.cross_slot = None
+
+    def views(self, lo: int, hi: int, t: int, layers: int) -> List[Tuple[torch.Tensor, torch.Tensor]]:
+        """Per-layer (K, V) [hi - lo, H, t, D] of slots lo..hi-1."""
+        return [(self.buf[lo:hi, l, 0, :, :t], self.buf[lo:hi, l, 1, :, :t]) for l in range(layers)]
+
+
+def _slot_runs(reqs: List["DualCacheRequest"], slot_of) -> List[List["DualCacheRequest"]]:
+    """reqs in slot order, cut where the slots stop being consecutive."""
+    runs: List[List[DualCacheRequest]] = []
+    for r in sorted(reqs, key=slot_of):
+        if runs and slot_of(r) == slot_of(runs[-1][-1]) + 1:
+            runs[-1].append(r)
+        else:
+            runs.append([r])
+    return runs
 
 
 class PhaseAwareSpeechScheduler:
@@ -183,6 +213,9 @@ class PhaseAwareSpeechScheduler:
         graph_max_blocks: int = 64,
     ):
         self.model = model
+        # Models with the paged step take a PagedKVCache as decode_step's past_key_values; a model
+        # that exposes only the reference's decode_step is served on gathered contiguous K/V.
+        self._paged_model = callable(getattr(model, "decode_step_paged", None))
         self.dual_cache = dual_cache_manager
         self.memory_guard = memory_guard or MemoryGuard()
         self.max_batch_size = max_batch_size
@@ -458,22 +491,22 @@ class PhaseAwareSpeechScheduler:
             req.graph_slot_reused = self.graph_buffers.slots[slot].reused
         else:
             if req.encoder_block_table:
-                s, _ = self.cross_arena.put_from_pool(enc_bm, req.encoder_block_table, t_enc,
-                                                      min(self.model.num_decoder_layers, enc_bm.num_layers))
+                self.cross_arena.put_from_pool(req, enc_bm, req.encoder_block_table, t_enc,
+                                               min(self.model.num_decoder_layers, enc_bm.num_layers))
             else:
-                s, _ = self.cross_arena.put(encoder_kv_list)
-            req.cross_slot = s
+                self.cross_arena.put(req, encoder_kv_list)
         self.active_encode.append(req)
 
     def _prefill_admitted(self, reqs: List[DualCacheRequest]) -> None:
         """Prefill the prompts of the requests placed in this step and emit their first tokens.
 
-        The reference prefills each request alone and reads its first token back with .item()
-        (phase_aware_scheduler.py:664-703). Here the requests that share a prompt length and a
-        cross-attention layer count run as one batch: one decode_step_paged over B x P prompt tokens
-        (fused causal append into each request's blocks) and one token readback per batch. A batch
-        that fails fails its requests, like a failed decode step. First tokens are then emitted in
-        admission order."""
+        The reference prefills each request alone through model.decode_step and reads its first
+        token back with .item() (phase_aware_scheduler.py:664-703). Here the requests that share a
+        prompt length and a cross-attention layer count, and whose encoder K/V sit in consecutive
+        slots, run as one batch: one model.decode_step over B x P prompt tokens (with a
+        PagedKVCache, the K/V go into each request's blocks in the attention launch) and one token
+        readback per batch. A batch that fails fails its requests, like a failed decode step. First
+        tokens are then emitted in admission order."""
         groups: Dict[Tuple[int, int, bool], List[DualCacheRequest]] = {}
         for r in reqs:
             # A graph slot holds at most max_enc_len encoder positions; a longer encoder output
@@ -512,46 +545,83 @@ class PhaseAwareSpeechScheduler:
                 req.cached_encoder_kv = None
 
     def _prefill(self, reqs: List[DualCacheRequest], p: int, layers: int, direct: bool) -> List[int]:
-        """One batched prefill of len(reqs) prompts of p tokens; returns each request's first token."""
+        """Prefill len(reqs) prompts of p tokens; returns each request's first token (in the order of reqs).
+        One decode_step per run of requests whose encoder K/V occupy consecutive slots."""
+        if direct:
+            runs = [[r] for r in reqs]
+        elif self.graph_decode:
+            runs = _slot_runs(reqs, lambda r: r.slot_idx)
+        else:
+            runs = _slot_runs(reqs, lambda r: r.cross_slot)
+        first: Dict[int, int] = {}
+        for run in runs:
+            first.update(zip(map(id, run), self._prefill_run(run, p, layers, direct)))
+        return [first[id(r)] for r in reqs]
+
+    def _encoder_inputs(self, run: List[DualCacheRequest], layers: int, direct: bool):
+        """The run's encoder K/V as decode_step takes them: per layer (K, V) [n, H, T, D] (views of the
+        slots), and the per-row lengths."""
+        n = len(run)
+        if direct:  # one request whose encoder output is longer than a graph slot: its own tensors
+            kv = run[0].cached_encoder_kv[:layers]
+            return [(k, v) for k, v in kv], [kv[0][0].shape[2]]
+        if self.graph_decode:
+            gb = self.graph_buffers
+            lens = [min(r.encoder_seq_len, gb.max_enc_len) for r in run]
+            t, lo = max(lens), run[0].slot_idx
+            return [(gb.g_cross_kv[lo:lo + n, l, 0, :, :t], gb.g_cross_kv[lo:lo + n, l, 1, :, :t])
+                    for l in range(layers)], lens
+        lens = [r.encoder_seq_len for r in run]
+        return self.cross_arena.views(run[0].cross_slot, run[0].cross_slot + n, max(lens), layers), lens
+
+    @staticmethod
+    def _encoder_mask(lens: List[int], lens_dev: torch.Tensor) -> Optional[torch.Tensor]:
+        """The reference's bool encoder mask [n, 1, 1, T] when the rows' encoder lengths differ
+        (phase_aware_scheduler.py:884-887), else None."""
+        if min(lens) == max(lens):
+            return None
+        t = max(lens)
+        return (torch.arange(t, device=lens_dev.device)[None, :] < lens_dev[:, None]).view(len(lens), 1, 1, t)
+
+    def _prefill_run(self, run: List[DualCacheRequest], p: int, layers: int, direct: bool) -> List[int]:
         dec_bm = self.dual_cache.decoder_bm
-        n = len(reqs)
-        prompts = torch.cat([r.prompt_token_ids.reshape(1, p) for r in reqs]).to(self.device)
-        width = max(len(r.decoder_block_table) for r in reqs)
-        meta = torch.full((n * width + n,), -1, dtype=torch.int32)  # tables [n, width], then lengths [n]
-        for i, r in enumerate(reqs):
+        n = len(run)
+        prompts = torch.cat([r.prompt_token_ids.reshape(1, p) for r in run]).to(self.device)
+        enc_list, enc_lens = self._encoder_inputs(run, layers, direct)
+        width = max(len(r.decoder_block_table) for r in run)
+        meta = torch.full((n * width + 2 * n,), -1, dtype=torch.int32)  # tables [n, width], lengths, encoder lengths
+        for i, r in enumerate(run):
             meta[i * width: i * width + len(r.decoder_block_table)] = torch.tensor(r.decoder_block_table,
                                                                                    dtype=torch.int32)
-        meta[n * width:] = p
+        meta[n * width: n * width + n] = p
+        meta[n * width + n:] = torch.tensor(enc_lens, dtype=torch.int32)
         meta = meta.to(self.device)
-        kv = PagedKV(dec_bm.key_pool, dec_bm.value_pool, meta[: n * width].view(n, width), meta[n * width:], p)
-        if direct:
-            cross = self._direct_cross(reqs[0].cached_encoder_kv, reqs[0].encoder_seq_len)
-        elif self.graph_decode:
-            gb = self.graph_buffers
-            ids = torch.tensor([[r.slot_idx for r in reqs], [min(r.encoder_seq_len, gb.max_enc_len) for r in reqs]],
-                               dtype=torch.int32).to(self.device)
-            cross = CrossKV([gb.g_cross_kv[:, l, 0] for l in range(layers)],
-                            [gb.g_cross_kv[:, l, 1] for l in range(layers)], ids[1], gb.max_enc_len, slot_ids=ids[0])
-        else:
-            cross = self._arena_cross([r.cross_slot for r in reqs], [r.encoder_seq_len for r in reqs], layers)
+        enc_dev = meta[n * width + n:]
+        enc_mask = self._encoder_mask(enc_lens, enc_dev)
         with torch.no_grad():
-            logits = self.model.decode_step_paged(prompts, kv, cross)
-            return native.argmax(logits).tolist()
+            if self._paged_model:
+                cache = PagedKVCache(dec_bm.key_pool, dec_bm.value_pool, meta[: n * width].view(n, width),
+                                     meta[n * width: n * width + n], p, cross_lens=enc_dev, cross_mask=enc_mask)
+                out = self.model.decode_step(input_ids=prompts, past_key_values=cache, encoder_past_kv_list=enc_list,
+                                             encoder_attention_mask=enc_mask, use_cache=True, logits_to_keep=1)
+            else:
+                out = self.model.decode_step(input_ids=prompts, encoder_past_kv_list=enc_list,
+                                             encoder_attention_mask=enc_mask, use_cache=True)
+                self._append_prompt_kv(out.past_key_values, run, p)
+            return native.argmax(out.logits[:, -1, :]).tolist()
 
-    def _direct_cross(self, enc_kv: List[Tuple[torch.Tensor, torch.Tensor]], t_enc: int) -> CrossKV:
-        ks = [k for k, _ in enc_kv]
-        vs = [v for _, v in enc_kv]
-        for i, (k, v) in enumerate(zip(ks, vs)):
-            if k.stride(3) != 1 or k.stride() != v.stride():
-                ks[i], vs[i] = k.contiguous(), v.contiguous()
-        lens = torch.tensor([t_enc], dtype=torch.int32, device=self.device)
-        return CrossKV(ks, vs, lens, t_enc)
-
-    def _arena_cross(self, slots: List[int], lens: List[int], layers: int) -> CrossKV:
-        a = self.cross_arena
-        meta = torch.tensor([slots, lens], dtype=torch.int32).to(self.device, non_blocking=True)
-        return CrossKV([a.buf[:, l, 0] for l in range(layers)], [a.buf[:, l, 1] for l in range(layers)],
-                       meta[1], a.max_len, slot_ids=meta[0])
+    def _append_prompt_kv(self, cache, run: List[DualCacheRequest], p: int) -> None:
+        """Write the prompt K/V a contiguous-cache model returned ([n, H, P, D] per layer) into each
+        request's blocks, one skv_append per layer (the reference's block copies, :672-690)."""
+        dec_bm = self.dual_cache.decoder_bm
+        slots = torch.tensor([dec_bm.slot(r.decoder_block_table, i) for r in run for i in range(p)],
+                             dtype=torch.int64).to(self.device)
+        for l in range(dec_bm.num_layers):
+            k, v = cache.layers[l].keys, cache.layers[l].values
+            rows = k.shape[0] * p
+            native.append(k[:, :, -p:].permute(0, 2, 1, 3).reshape(rows, k.shape[1], k.shape[3]),
+                          v[:, :, -p:].permute(0, 2, 1, 3).reshape(rows, v.shape[1], v.shape[3]),
+                          dec_bm.key_pool[l], dec_bm.value_pool[l], slots)
 
     # ------------------------------------------------------------------ decode
     def _staging(self, n: int) -> torch.Tensor:
@@ -573,13 +643,10 @@ class PhaseAwareSpeechScheduler:
         t0 = time.perf_counter()
         dec_bm = self.dual_cache.decoder_bm
         bs = dec_bm.block_size
-        # Batch rows longest-first (evens the attention kernel's per-unit load);
-        # results go back to the requests, whose order is kept.
-        reqs = sorted(self.active_decode, key=lambda r: -r.decoder_seq_len)
         # Block-boundary allocation (reference :780-783), one request at a time: a request
         # that cannot get its next block fails alone and leaves the batch; the others decode.
         starved = []
-        for r in reqs:
+        for r in self.active_decode:
             if r.decoder_seq_len % bs == 0:
                 try:
                     r.decoder_block_table.append(self.dual_cache.allocate_decoder_block())
@@ -587,47 +654,23 @@ class PhaseAwareSpeechScheduler:
                     logger.error(f"request {r.id}: no decoder block for position {r.decoder_seq_len}: {e}")
                     starved.append(r)
         for r in starved:
-            reqs.remove(r)
             self._complete_request(r, status=RequestPhase.FAILED)
         if starved:
             self.active_decode = [r for r in self.active_decode if r not in starved]
-        if not reqs:
+        if not self.active_decode:
             return
+        tok_of: Dict[int, int] = {}
         try:
-            b = len(reqs)
-            maxblk = max(len(r.decoder_block_table) for r in reqs)
-            staging = self._staging(b * (maxblk + 4))
-            meta = staging.numpy()[: b * (maxblk + 4)].reshape(b, maxblk + 4)
-            meta.fill(-1)
-            for i, r in enumerate(reqs):
-                meta[i, :len(r.decoder_block_table)] = r.decoder_block_table
-                meta[i, maxblk] = r.decoder_seq_len + 1
-                meta[i, maxblk + 1] = r.encoder_seq_len
-                meta[i, maxblk + 2] = r.cross_slot
-                meta[i, maxblk + 3] = r.last_token_id
-            dev = staging[: b * (maxblk + 4)].view(b, maxblk + 4).to(self.device, non_blocking=True)
-            tables = dev[:, :maxblk].contiguous()
-            ctx = dev[:, maxblk].contiguous()
-            enc = dev[:, maxblk + 1].contiguous()
-            cslot = dev[:, maxblk + 2].contiguous()
-            ids = dev[:, maxblk + 3].to(torch.int64).view(b, 1)
-            a = self.cross_arena
-            layers = reqs[0].cross_layers
-            if any(r.cross_layers != layers for r in reqs):
-                raise RuntimeError("requests in one decode batch must have encoder K/V for the same layers")
-            cross = CrossKV([a.buf[:, l, 0] for l in range(layers)], [a.buf[:, l, 1] for l in range(layers)],
-                            enc, a.max_len, slot_ids=cslot)
-            kv = PagedKV(dec_bm.key_pool, dec_bm.value_pool, tables, ctx, int(meta[:, maxblk].max()))
-            with torch.no_grad():
-                logits = self.model.decode_step_paged(ids, kv, cross)
-                toks = native.argmax(logits).tolist()
+            # The batch in arena order: row b's encoder K/V is slot lo + b (one run when, as usual,
+            # the active requests hold slots 0..B-1).
+            for run in _slot_runs(self.active_decode, lambda r: r.cross_slot):
+                tok_of.update(zip(map(id, run), self._decode_run(run)))
         except Exception as e:  # the batched step failed: release every request deterministically
             logger.error(f"batched decode step failed, releasing its requests: {e}", exc_info=True)
-            for r in list(reqs):
+            for r in list(self.active_decode):
                 self._complete_request(r, status=RequestPhase.FAILED)
             self.active_decode = []
             return
-        tok_of = {id(r): tok for r, tok in zip(reqs, toks)}
         still = []
         for r in self.active_decode:
             tok = tok_of[id(r)]
@@ -642,6 +685,73 @@ class PhaseAwareSpeechScheduler:
         self.active_decode = still
         self.decode_steps += 1
         self.decode_time_s += time.perf_counter() - t0
+
+    def _decode_run(self, run: List[DualCacheRequest]) -> List[int]:
+        """One decode step of the requests of run (encoder K/V in consecutive arena slots) through
+        model.decode_step, as the reference's eager step (phase_aware_scheduler.py:982-991); returns
+        each request's greedy token."""
+        dec_bm = self.dual_cache.decoder_bm
+        b = len(run)
+        layers = run[0].cross_layers
+        if any(r.cross_layers != layers for r in run):
+            raise RuntimeError("requests in one decode batch must have encoder K/V for the same layers")
+        maxblk = max(len(r.decoder_block_table) for r in run)
+        staging = self._staging(b * (maxblk + 4))
+        meta = staging.numpy()[: b * (maxblk + 4)].reshape(b, maxblk + 4)
+        meta.fill(-1)
+        for i, r in enumerate(run):
+            meta[i, :len(r.decoder_block_table)] = r.decoder_block_table
+            meta[i, maxblk] = r.decoder_seq_len + 1
+            meta[i, maxblk + 1] = r.encoder_seq_len
+            meta[i, maxblk + 2] = r.decoder_seq_len
+            meta[i, maxblk + 3] = r.last_token_id
+        dev = staging[: b * (maxblk + 4)].view(b, maxblk + 4).to(self.device, non_blocking=True)
+        tables = dev[:, :maxblk].contiguous()
+        ctx = dev[:, maxblk].contiguous()
+        enc = dev[:, maxblk + 1].contiguous()
+        pos = dev[:, maxblk + 2: maxblk + 3].to(torch.int64)
+        ids = dev[:, maxblk + 3: maxblk + 4].to(torch.int64)
+        enc_lens = [r.encoder_seq_len for r in run]
+        enc_list = self.cross_arena.views(run[0].cross_slot, run[0].cross_slot + b, max(enc_lens), layers)
+        enc_mask = self._encoder_mask(enc_lens, enc)
+        with torch.no_grad():
+            if self._paged_model:
+                cache = PagedKVCache(dec_bm.key_pool, dec_bm.value_pool, tables, ctx, int(meta[:, maxblk].max()),
+                                     cross_lens=enc, cross_mask=enc_mask)
+                out = self.model.decode_step(input_ids=ids, past_key_values=cache, encoder_past_kv_list=enc_list,
+                                             attention_mask=None, encoder_attention_mask=enc_mask, position_ids=pos,
+                                             use_cache=True, logits_to_keep=1)
+            else:
+                out = self._decode_run_contiguous(run, tables, ctx, ids, pos, enc_list, enc_mask)
+            return native.argmax(out.logits[:, -1, :]).tolist()
+
+    def _decode_run_contiguous(self, run, tables, ctx, ids, pos, enc_list, enc_mask):
+        """A model with only the reference's decode_step: each row's past K/V is gathered from the pool
+        into a zero-padded [B, H, T, D] batch (skv_gather) with the reference's padding mask
+        (:818-846), the model steps, and the new token's K/V goes back into the pool (skv_append)
+        from the returned cache (:1001-1010)."""
+        dec_bm = self.dual_cache.decoder_bm
+        seq = [r.decoder_seq_len for r in run]
+        tmax = max(seq)
+        past = ctx - 1
+        cache = KVCache([LayerKV(*native.gather(dec_bm.key_pool[l], dec_bm.value_pool[l], tables, past, tmax))
+                         for l in range(dec_bm.num_layers)])
+        mask = None
+        if len(run) > 1 and min(seq) < tmax:
+            m = torch.ones((len(run), tmax + 1), dtype=torch.long)
+            for i, n in enumerate(seq):
+                m[i, n:tmax] = 0
+            mask = m.to(self.device)
+        out = self.model.decode_step(input_ids=ids, past_key_values=cache, encoder_past_kv_list=enc_list,
+                                     attention_mask=mask, encoder_attention_mask=enc_mask, position_ids=pos,
+                                     use_cache=True)
+        slots = torch.tensor([dec_bm.slot(r.decoder_block_table, r.decoder_seq_len) for r in run],
+                             dtype=torch.int64).to(self.device)
+        for l in range(dec_bm.num_layers):
+            layer = out.past_key_values.layers[l]
+            native.append(layer.keys[:, :, -1, :], layer.values[:, :, -1, :], dec_bm.key_pool[l],
+                          dec_bm.value_pool[l], slots)
+        return out
 
     def _process_decode_phase_graph(self) -> None:
         gb = self.graph_buffers
@@ -698,9 +808,8 @@ class PhaseAwareSpeechScheduler:
                     if all(self.dual_cache.encoder_bm.ref_counts[b] == 0 for b in entry["block_table"]):
                         self._full_input_enc_cache.pop(req.full_input_hash, None)
                 req.encoder_block_table = []
-            if req.cross_slot is not None and self.cross_arena is not None:
-                self.cross_arena.release(req.cross_slot)
-                req.cross_slot = None
+            if self.cross_arena is not None:
+                self.cross_arena.release(req)
         finally:
             req.cached_decoder_kv = None
             req.cached_encoder_kv = None

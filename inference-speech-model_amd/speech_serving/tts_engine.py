@@ -38,7 +38,7 @@ import torch
 
 from . import native
 from .block_manager import BlockManager
-from .models import PagedKV, StreamingMultiCodebookTTSModel
+from .models import KVCache, LayerKV, PagedKV, PagedKVCache, StreamingMultiCodebookTTSModel
 
 
 @dataclass
@@ -65,11 +65,20 @@ class StreamingTTSEngine:
     """Continuous batching of streaming multi-codebook TTS requests over a paged KV pool."""
 
     def __init__(self, model: StreamingMultiCodebookTTSModel, block_manager: BlockManager, max_batch_size: int = 8,
-                 device: str = "cuda", graph_decode: bool = True):
+                 device: str = "cuda", graph_decode: Optional[bool] = None):
         self.model = model
         self.block_manager = block_manager
         self.max_batch_size = max_batch_size
         self.device = device
+        # The model is called as the reference calls it, model(input_codebooks, past_key_values, use_cache)
+        # (tts_engine.py:188): models with the paged step get a PagedKVCache; a model with only that
+        # forward is served on K/V gathered from the pool, one request at a time, as the reference does.
+        self._paged_model = callable(getattr(model, "decode_step_paged", None))
+        if graph_decode is None:
+            graph_decode = self._paged_model
+        if graph_decode and not self._paged_model:
+            raise TypeError(f"graph decode captures the model's paged step (decode_step_paged); "
+                            f"{type(model).__name__} has none: use graph_decode=False")
         self.graph_decode = graph_decode
 
         self.active: List[TTSRequest] = []
@@ -162,27 +171,64 @@ class StreamingTTSEngine:
                     self._take_slot(req, frame)
                 self.active.append(req)
 
-    def _paged_kv(self, tables: List[List[int]], ctx: List[int]) -> PagedKV:
+    def _paged_cache(self, tables: List[List[int]], ctx: List[int]) -> PagedKVCache:
         bm = self.block_manager
         width = max(len(t) for t in tables)
         rows = [t + [0] * (width - len(t)) for t in tables]  # padding past a row's keys is never read
         dev = bm.key_pool[0].device
-        return PagedKV(bm.key_pool, bm.value_pool, torch.tensor(rows, dtype=torch.int32).to(dev),
-                       torch.tensor(ctx, dtype=torch.int32).to(dev), max(ctx))
+        return PagedKVCache(bm.key_pool, bm.value_pool, torch.tensor(rows, dtype=torch.int32).to(dev),
+                            torch.tensor(ctx, dtype=torch.int32).to(dev), max(ctx))
 
     @torch.no_grad()
     def _prefill(self, req: TTSRequest) -> torch.Tensor:
         """Prompt forward: its K/V go into the request's blocks; returns the first frame [K]."""
-        kv = self._paged_kv([req.block_table], [req.seq_len])
-        logits = self.model.decode_step_paged(req.prompt_codebooks.unsqueeze(0), kv)  # [1, K, V]
-        return self._greedy(logits)[0]
+        codes = req.prompt_codebooks.unsqueeze(0)
+        if self._paged_model:
+            out = self.model(input_codebooks=codes, past_key_values=self._paged_cache([req.block_table],
+                                                                                     [req.seq_len]),
+                             use_cache=True, logits_to_keep=1)
+        else:
+            out = self.model(input_codebooks=codes, past_key_values=None, use_cache=True)
+            self._append_kv(out.past_key_values, [req], 0, req.seq_len)
+        return self._greedy(out.logits[:, -1])[0]
 
     @torch.no_grad()
-    def _decode(self, batch: List[TTSRequest]) -> torch.Tensor:
-        """One frame for every request of the batch: [B, K] codebook tokens."""
-        kv = self._paged_kv([r.block_table for r in batch], [r.seq_len + 1 for r in batch])
+    def _decode(self, batch: List[TTSRequest]) -> List[torch.Tensor]:
+        """One frame for every request of the batch: [K] codebook tokens each."""
+        if not self._paged_model:
+            return [self._decode_contiguous(r) for r in batch]
+        cache = self._paged_cache([r.block_table for r in batch], [r.seq_len + 1 for r in batch])
         inputs = torch.cat([r.last_frame_codebooks for r in batch], dim=0)  # [B, 1, K]
-        return self._greedy(self.model.decode_step_paged(inputs, kv))
+        out = self.model(input_codebooks=inputs, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        return list(self._greedy(out.logits[:, -1]).unbind(0))
+
+    def _decode_contiguous(self, req: TTSRequest) -> torch.Tensor:
+        """The reference's step for one request (tts_engine.py:174-204): its history gathered out of the
+        pool (skv_gather), the model forward on that contiguous cache, the new frame's K/V appended into
+        the pool (skv_append)."""
+        bm = self.block_manager
+        dev = bm.key_pool[0].device
+        table = torch.tensor([req.block_table], dtype=torch.int32, device=dev)
+        lens = torch.tensor([req.seq_len], dtype=torch.int32, device=dev)
+        cache = KVCache([LayerKV(*native.gather(bm.key_pool[l], bm.value_pool[l], table, lens, req.seq_len))
+                         for l in range(bm.num_layers)])
+        out = self.model(input_codebooks=req.last_frame_codebooks, past_key_values=cache, use_cache=True)
+        self._append_kv(out.past_key_values, [req], req.seq_len, 1)
+        return self._greedy(out.logits[:, -1])[0]
+
+    def _append_kv(self, cache, reqs: List[TTSRequest], start: int, n: int) -> None:
+        """Append the last n positions of each layer's returned K/V ([B, H, T, D]) at positions
+        start..start+n-1 of each request's blocks (the reference's block writes, :191-198)."""
+        bm = self.block_manager
+        dev = bm.key_pool[0].device
+        slots = torch.tensor([bm.slot(r.block_table, start + i) for r in reqs for i in range(n)],
+                             dtype=torch.int64).to(dev)
+        for l in range(bm.num_layers):
+            k, v = cache.layers[l].keys[:, :, -n:], cache.layers[l].values[:, :, -n:]
+            rows = k.shape[0] * n
+            native.append(k.permute(0, 2, 1, 3).reshape(rows, k.shape[1], k.shape[3]),
+                          v.permute(0, 2, 1, 3).reshape(rows, v.shape[1], v.shape[3]),
+                          bm.key_pool[l], bm.value_pool[l], slots)
 
     def _greedy(self, logits: torch.Tensor) -> torch.Tensor:
         """Argmax per (request, codebook) row of logits [B, K, V] -> int64 [B, K]."""

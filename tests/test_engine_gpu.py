@@ -351,7 +351,7 @@ def test_failed_decode_step_releases_everything(cuda):
     done = s.run_until_done()
     assert len(done) == 2 and all(r.phase == RequestPhase.FAILED for r in done)
     assert dec.allocated_block_count == 0 and enc.allocated_block_count == 0
-    assert s.cross_arena.live == {}
+    assert s.cross_arena.owner == [] and s.cross_arena.lens == []
 
 
 @pytest.mark.parametrize("mode", ["eager", "graph"])
@@ -381,7 +381,7 @@ def test_failed_batched_prefill_fails_its_requests_and_releases_everything(cuda,
     if mode == "graph":
         assert s.graph_buffers.active_slot_count() == 0
     else:
-        assert s.cross_arena.live == {}
+        assert s.cross_arena.owner == [] and s.cross_arena.lens == []
     s.submit(torch.randn(80, 64).to(cuda), max_new_tokens=6)
     done = s.run_until_done()
     assert done[-1].phase == RequestPhase.COMPLETED and len(done[-1].generated_tokens) == 6

@@ -163,3 +163,40 @@ def test_state_dict_names_match_reference_layout():
               "decoder_layers.0.mlp.0.weight", "decoder_layers.0.mlp.2.bias", "decoder_norm.weight",
               "lm_head.weight"]:
         assert k in keys, k
+
+
+def test_cross_arena_keeps_live_requests_in_the_leading_slots():
+    """The eager encoder K/V arena: requests take slots 0, 1, 2, ...; a released slot is refilled by the
+    last live request (its K/V moved, its cross_slot updated), so a batch in slot order is the views
+    buf[0:n]; the T dimension grows with the live slots' contents kept."""
+    from types import SimpleNamespace
+
+    from speech_serving.phase_aware_scheduler import CrossArena, _slot_runs
+
+    a = CrossArena(4, 2, 2, 8, torch.float32, torch.device("cpu"))
+    reqs = [SimpleNamespace(id=i, cross_slot=None) for i in range(4)]
+    kvs = []
+    for i, r in enumerate(reqs[:3]):
+        t = 5 + i
+        kv = [(torch.full((1, 2, t, 8), 10.0 * i + l), torch.full((1, 2, t, 8), -10.0 * i - l)) for l in range(2)]
+        kvs.append(kv)
+        assert a.put(r, kv) == i and r.cross_slot == i
+    a.release(reqs[0])  # the last live request moves into slot 0
+    assert reqs[0].cross_slot is None and reqs[2].cross_slot == 0 and reqs[1].cross_slot == 1
+    assert a.owner == [reqs[2], reqs[1]] and a.lens == [7, 6]
+    views = a.views(0, 2, 7, 2)
+    for l in range(2):
+        assert torch.equal(views[l][0][0], kvs[2][l][0][0]) and torch.equal(views[l][1][0], kvs[2][l][1][0])
+        assert torch.equal(views[l][0][1, :, :6], kvs[1][l][0][0])
+    a.release(reqs[2])  # releasing the last slot moves nothing
+    assert a.owner == [reqs[1]] and reqs[1].cross_slot == 0
+    a.release(reqs[2])  # a second release is a no-op
+    big = [(torch.ones(1, 2, 1600, 8), torch.ones(1, 2, 1600, 8)) for _ in range(2)]
+    assert a.put(reqs[3], big) == 1 and a.max_len >= 1600  # grown, slot 0 kept
+    assert torch.equal(a.views(0, 1, 6, 2)[1][0][0], kvs[1][1][0][0])
+    with pytest.raises(RuntimeError, match="full"):
+        for r in [SimpleNamespace(id=9, cross_slot=None) for _ in range(3)]:
+            a.put(r, big)
+    # batches split where the slots stop being consecutive
+    rs = [SimpleNamespace(s=s) for s in (4, 0, 1, 3, 7, 2)]
+    assert [[r.s for r in run] for run in _slot_runs(rs, lambda r: r.s)] == [[0, 1, 2, 3, 4], [7]]

@@ -91,24 +91,24 @@ def test_cross_kv_and_sampling_flags_do_not_change_tokens(cuda, flags):
 
 
 def test_generation_stops_on_eos_with_a_task_prompt(cuda):
-    """EOS forced from the third model call on (one batched prefill, then decode steps): the request
-    ends at EOS, well before max_new_tokens, keeps EOS as its last token (eager decode) and frees
-    its blocks."""
+    """EOS forced from the third model.decode_step call on (the prefill, then decode steps), by wrapping
+    decode_step as the reference's test does: the request ends at EOS, well before max_new_tokens, keeps
+    EOS as its last token (eager decode) and frees its blocks."""
     eos = 42
     m = tiny(cuda, vocab=512)
     s, enc, dec = scheduler(m, cuda, max_batch_size=2, eos_token_id=eos)
-    real = m.decode_step_paged
+    real = m.decode_step
     n = [0]
 
     def forced(*a, **k):
-        logits = real(*a, **k)
+        out = real(*a, **k)
         n[0] += 1
         if n[0] >= 3:
-            logits = torch.full_like(logits, -1e4)
-            logits[:, eos] = 1e4
-        return logits
+            out.logits[:, -1, :] = -1e4
+            out.logits[:, -1, eos] = 1e4
+        return out
 
-    m.decode_step_paged = forced
+    m.decode_step = forced
     s.submit(torch.randn(80, 32).to(cuda), prompt_token_ids=torch.tensor([[1, 2, 3]]), max_new_tokens=50)
     (r,) = s.run_until_done()
     assert r.phase == RequestPhase.COMPLETED

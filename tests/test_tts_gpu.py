@@ -107,6 +107,70 @@ def test_frames_match_reference_engine(cuda, graph):
     assert tables == history
 
 
+class HookOnlyTTSModel:
+    """A TTS model that offers the engine only the reference's call, model(input_codebooks,
+    past_key_values, use_cache) on contiguous K/V (tts_engine.py:188), and the attributes it reads."""
+
+    def __init__(self, m):
+        self._m = m
+        for a in ("num_layers", "num_heads", "head_dim", "hidden_dim", "num_codebooks", "vocab_size", "config"):
+            setattr(self, a, getattr(m, a))
+        self.calls = 0
+
+    def __call__(self, input_codebooks, past_key_values=None, use_cache=True):
+        self.calls += 1
+        return self._m(input_codebooks, past_key_values=past_key_values, use_cache=use_cache)
+
+
+def test_hook_only_model_frames_match_reference_engine(cuda):
+    """A model with only the reference's forward is served as the reference serves it (per request:
+    history gathered out of the pool, forward, new K/V appended): the golden frames and block tables;
+    graph decode, which captures the paged step, refuses it."""
+    z, cfg, m = _golden(cuda)
+    bm = _bm(cfg, cuda)
+    model = HookOnlyTTSModel(m)
+    with pytest.raises(TypeError, match="graph_decode=False"):
+        StreamingTTSEngine(model, bm, max_batch_size=cfg["max_batch"], device=str(cuda), graph_decode=True)
+    engine = StreamingTTSEngine(model, bm, max_batch_size=cfg["max_batch"], device=str(cuda))
+    assert not engine.graph_decode
+    for r in range(cfg["requests"]):
+        engine.submit(torch.from_numpy(z["prompts"][r]), max_new_frames=cfg["frames"])
+    done = engine.run_until_done()
+    assert [q.id for q in done] == [0, 1, 2]
+    for q in done:
+        assert np.array_equal(torch.stack(q.generated_frames).cpu().numpy(), z[f"engine_frames{q.id}"]), q.id
+    assert model.calls == cfg["requests"] * cfg["frames"]  # one prefill and frames - 1 steps per request
+    assert [bm.allocated_block_count, bm.num_free_blocks] == z["engine_blocks"].tolist()
+
+
+def test_forward_wrapper_sees_every_eager_step(cuda):
+    """Eager decode of a paged model goes through model(...) too: a wrapper that forces codebook 0 to
+    token 3 from the second call on changes every later frame's first token, as it would in the
+    reference's engine."""
+    z, cfg, m = _golden(cuda)
+    bm = _bm(cfg, cuda)
+    engine = StreamingTTSEngine(m, bm, max_batch_size=cfg["max_batch"], device=str(cuda), graph_decode=False)
+    real = m.forward
+    n = [0]
+
+    def forced(*a, **k):
+        out = real(*a, **k)
+        n[0] += 1
+        if n[0] >= 2:
+            out.logits[:, -1, 0, :] = -1e4
+            out.logits[:, -1, 0, 3] = 1e4
+        return out
+
+    m.forward = forced
+    engine.submit(torch.from_numpy(z["prompts"][0]), max_new_frames=cfg["frames"])
+    (q,) = engine.run_until_done()
+    m.forward = real
+    frames = torch.stack(q.generated_frames).cpu().numpy()
+    assert n[0] == cfg["frames"]
+    assert (frames[1:, 0] == 3).all()
+    assert np.array_equal(frames[0], z["engine_frames0"][0])
+
+
 def test_prefill_and_step_logits_match_reference(cuda):
     z, cfg, model = _golden(cuda)
     bm = _bm(cfg, cuda)
