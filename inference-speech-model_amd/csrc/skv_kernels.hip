@@ -646,6 +646,7 @@ constexpr int kMaxChunkBlocks = 256;    // LDS block-id slots per chunk
 constexpr int kPartPad = 4;             // partial record = m, l, pad, pad, acc[D]
 // s_waitcnt immediate for vmcnt(0) alone (expcnt and lgkmcnt at their maxima).
 constexpr int kWaitVmcnt0 = 0x0f70;
+constexpr int kRankRows = 64;  // most rows a launch ranks by length (one per lane of a wave)
 
 struct AttnParams {
   const uint4* q;  // strides below are in 16-byte vector units
@@ -684,6 +685,9 @@ struct AttnParams {
   // row = umulhi(item, heads_magic), exact for items * heads < 2^32.
   int32_t snake, cu_shift;
   uint32_t items, heads_magic;
+  // Rank order (paged, snake, q_len 1, at most kRankRows rows): item rows are ranks by length, so the
+  // snake order balances the units' bytes whatever order the caller's rows come in.
+  int32_t rank;
   float scale_log2;
   float* part;  // [rows*heads*nchunk_max][D + kPartPad]
 };
@@ -814,7 +818,7 @@ __device__ __forceinline__ uint4 load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off
 // scalar registers when the wave starts, so the chain's first memory access
 // (block table, row length) does not wait for a kernel-argument load.
 // qlen_group: q_len in bits 0-15, query heads per KV head in bits 16-31.
-// flags: bit 0 grid3d, bit 1 snake order, bit 2 causal, bits 8-15 cu_shift,
+// flags: bit 0 grid3d, bit 1 snake order, bit 2 causal, bit 3 rank order, bits 8-15 cu_shift,
 // bits 16-23 log2(block size) (the fast path's power-of-two block size).
 // The paged variants are built for at least 5 waves per SIMD, the register
 // budget of 5 resident workgroups per CU (a large decode batch's launch is one
@@ -837,6 +841,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
   // Fast paged path: the fused-append K/V row, copied here by the load itself
   // (one 16-byte slot per lane of the last wave).
   __shared__ uint4 s_new[(PAGED && FAST) ? 2 : 1][64];
+  __shared__ int s_ranked_row;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -857,6 +862,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
   // the CU's one scalar unit before its first memory access, so the common
   // shapes (q_len 1, no KV grouping, one chunk) take no integer division.
   int h, row, chunk;
+  int ranked_len = 0;  // rank order: the row's length, as the ranking read it
   if (flags & 2u) {
     const uint32_t w = bx + blockIdx.y * (uint32_t)heads;
     const uint32_t round = (1u << cu_shift) - 1u;
@@ -869,6 +875,48 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
     row = (int)__umulhi(item, heads_magic);
     h = (int)item - row * heads;
     chunk = 0;
+    if constexpr (PAGED) {
+      // Rank order: `row` is a rank, and the workgroup takes the row whose length has that rank
+      // (longest first, ties to the lower row). Every wave reads the lengths, one row per lane,
+      // with a buffer load (lanes past the batch read zero; the batch is items / heads, exact as
+      // for the row above). Rows already longest-first need nothing more: the rank is the row.
+      // Otherwise wave 0 selects the row, a radix selection over the length bits with wave
+      // ballots and then the rank's place among equal lengths, and hands it to the other waves
+      // through LDS.
+      if (flags & 8u) {
+        const uint32_t nrows = __umulhi(items, heads_magic);
+        const __amdgpu_buffer_rsrc_t lres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(a_lens), (short)0, (int)(nrows * 4u), kBufWord3);
+        const int lraw = (int)__builtin_amdgcn_raw_buffer_load_b32(lres, (uint32_t)lane * 4u, 0, 0);
+        // The parameter-block fields of the address chain load while the lengths are in flight.
+        asm volatile("" ::"s"(p.q), "s"(p.qsb), "s"(p.qsq), "s"(p.qsh), "s"(p.osb), "s"(p.osq), "s"(p.osh),
+                     "s"(p.k), "s"(p.v), "s"(p.nb), "s"(p.row_vecs), "s"(p.kv_bytes), "s"(p.kn), "s"(p.vn),
+                     "s"(p.nsb), "s"(p.nsh), "s"(p.nchunk_max));
+        const int lenj = min(max(lraw, 0), max_len);
+        const int prev = __shfl_up(lenj, 1);
+        if (__any(lane > 0 && lenj > prev)) {  // the same in every wave (lanes past the batch hold 0)
+          if (__builtin_amdgcn_readfirstlane(wave) == 0) {
+            uint64_t cand = __ballot((uint32_t)lane < nrows);
+            uint32_t k = (uint32_t)row;
+            for (int bit = 31 - __clz(max(max_len, 1)); bit >= 0; --bit) {
+              const uint64_t ones = __ballot((lenj >> bit) & 1) & cand;
+              const uint32_t c = (uint32_t)__popcll(ones);
+              if (k < c) {
+                cand = ones;
+              } else {
+                k -= c;
+                cand &= ~ones;
+              }
+            }
+            for (; k > 0; --k) cand &= cand - 1;  // the k-th lowest row of the remaining length
+            if (lane == 0) s_ranked_row = __ffsll((unsigned long long)cand) - 1;
+          }
+          lds_barrier();
+          row = __builtin_amdgcn_readfirstlane(s_ranked_row);
+        }
+        ranked_len = __builtin_amdgcn_readlane(lraw, row);
+      }
+    }
   } else if (flags & 1u) {
     h = bx;
     row = blockIdx.y;
@@ -903,7 +951,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
   // span up to max_len (inside the table row, which covers max_len), so the
   // staging does not wait for the row length. The fast path reads block ids
   // per wave with scalar loads in its key loop instead.
-  int row_len = a_lens[b];
+  int row_len = PAGED && (flags & 8u) ? ranked_len : a_lens[b];
   const int trow = PAGED && a_trows ? a_trows[b] : b;
   asm("" : "+s"(row_len)
       : "s"(trow), "s"(p.q), "s"(p.qsb), "s"(p.qsq), "s"(p.qsh), "s"(p.osb), "s"(p.osq), "s"(p.osh),
@@ -2127,7 +2175,8 @@ void launch_attention(const AttnParams& p, hipStream_t stream) {
   const bool fast = p.kv_bytes <= kBufLimit && (!PAGED || (p.bs_shift >= 0 && (1 << p.bs_shift) >= kTpi));
   const uint32_t qlen_group = (uint32_t)p.qlen | ((uint32_t)p.group << 16);
   const uint32_t flags = (p.grid3d ? 1u : 0u) | (p.snake ? 2u : 0u) | (p.causal ? 4u : 0u) |
-                         ((uint32_t)p.cu_shift << 8) | ((uint32_t)(p.bs_shift & 0xff) << 16);
+                         (PAGED && p.rank ? 8u : 0u) | ((uint32_t)p.cu_shift << 8) |
+                         ((uint32_t)(p.bs_shift & 0xff) << 16);
   if (fast) {
     hipLaunchKernelGGL((attention_kernel<DT, D, PAGED, true>), grid, dim3(64 * kWaves), 0, stream, p.tables, p.lens,
                        p.trows, p.heads, p.tstride, p.max_len, p.chunk, qlen_group, flags, p.items, p.heads_magic, p);
@@ -2641,6 +2690,7 @@ int paged_attention_impl(const char* who, const void* q, int64_t q_stride_b, int
     p.nchunk_max = 1;
     p.snake = 0;
   }
+  p.rank = p.snake && q_len == 1 && batch <= kRankRows;
   rc = bind_workspace(p, who, head_dim, workspace, ws_bytes);
   if (rc != SKV_OK) {
     if (!fixed_scratch) return rc;

@@ -1,10 +1,10 @@
 """Serving scenarios of the benchmark configurations, end to end on the GPU.
 
-  C3  Whisper-base-shaped decoder (6 layers, d_model 512, 8 heads x 64, fp16), 32 requests whose
-      encoder outputs have valid lengths U[500, 1500] (the explicit cross-attention mask of the
-      reference, expressed as per-request lengths), 224 greedy tokens, continuous batching with
-      graph-slot reuse. The scenario runs on 16 slots: 32 requests on 32 slots would never reuse a
-      slot, which the configuration asks for. Graph decode must give the eager decode's tokens.
+  C3  Whisper-base-shaped decoder (6 layers, d_model 512, 8 heads x 64, fp16) at batch 32: 32 slots
+      serving 64 requests whose encoder outputs have valid lengths U[500, 1500] (the explicit
+      cross-attention mask of the reference, expressed as per-request lengths), 224 greedy tokens
+      each, continuous batching with graph-slot reuse (the second 32 requests take the slots the
+      first 32 free). Graph decode must give the eager decode's tokens.
   C4  Whisper-small-shaped decoder (12 layers, d_model 768, 12 heads x 64, bf16), 64 graph slots with
       batch buckets 1/8/16/32/64, Poisson arrivals (lambda = 4 req/s on a simulated clock) of 200
       requests with output lengths U[16, 448], readback every 4 steps.
@@ -79,19 +79,20 @@ def encoder_kv(m, cuda, t, seed):
 def test_c3_base_variable_encoder_lengths_graph_matches_eager(cuda):
     dt = torch.float16
     m = model(cuda, 6, 512, 8, 51865, dt, seed=3)
-    lengths = np.random.default_rng(3).integers(500, 1501, size=32).tolist()
+    lengths = np.random.default_rng(3).integers(500, 1501, size=64).tolist()
     kvs = [encoder_kv(m, cuda, t, 100 + i) for i, t in enumerate(lengths)]
     results = {}
     for mode in ("eager", "graph"):
         enc, dec = managers(m, cuda, dt, dec_blocks=512)
         kw = dict(graph_decode=True, graph_readback_k=4, graph_direct_encoder_kv=True, graph_max_enc_len=1500) \
             if mode == "graph" else {}
-        s = PhaseAwareSpeechScheduler(m, DualCacheManager(enc, dec), QUEUE_ALL, max_batch_size=16,
+        s = PhaseAwareSpeechScheduler(m, DualCacheManager(enc, dec), QUEUE_ALL, max_batch_size=32,
                                       device=str(cuda), eos_token_id=-1, **kw)
         for kv in kvs:
             s.submit_encoded(kv, prompt_token_ids=torch.tensor([PROMPT]), max_new_tokens=224)
         done = sorted(s.run_until_done(), key=lambda r: r.id)
-        assert len(done) == 32 and all(r.phase == RequestPhase.COMPLETED for r in done)
+        assert len(done) == 64 and all(r.phase == RequestPhase.COMPLETED for r in done)
+        assert s.peak_in_flight_requests == 32
         assert all(len(r.generated_tokens) == 224 for r in done)
         assert [r.encoder_seq_len for r in done] == lengths
         assert dec.allocated_block_count == 0 and enc.allocated_block_count == 0

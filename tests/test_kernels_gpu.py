@@ -405,3 +405,55 @@ def test_graph_replay_matches_eager(cuda):
         assert torch.equal(gs, out_s) and torch.equal(gc, out_c), f"replay {it} differs from eager"
         want = O.paged_attention(f64(q)[:, None], f64(kp), f64(vp), tb.numpy(), (pos + 1).tolist(), 0.125)[:, 0]
         assert_close(gs, want, torch.float16, f"graph replay {it}")
+
+
+# ------------------------------------------------------------------ row order
+@pytest.mark.parametrize("bsz,ties,trows", [(64, False, False), (64, True, False), (63, False, True), (65, False, False),
+                                            (20, True, True), (1, False, False)])
+def test_paged_attention_rows_in_any_order(cuda, bsz, ties, trows):
+    """A launch of up to 64 decode rows takes its (row, head) items in length order whatever order the rows
+    come in (more rows keep the given order): the same rows in any order give, row for row, the same bits
+    (outputs and appended pool rows), within the oracle bar. Ties: lengths from a few values; rows past the
+    table's reach clamp to it."""
+    gen = torch.Generator().manual_seed(700 + bsz + 2 * ties + trows)
+    h, d, bs, dtype, max_ctx = 20, 64, 16, torch.bfloat16, 452
+    maxblk = -(-max_ctx // bs)
+    nb = bsz * maxblk + 16
+    if ties:
+        ctx = torch.tensor([1, 7, 200, 452])[torch.randint(0, 4, (bsz,), generator=gen)]
+    else:
+        ctx = torch.randint(1, max_ctx + 1, (bsz,), generator=gen)
+    tables = torch.randperm(nb, generator=gen)[: bsz * maxblk].view(bsz, maxblk).to(torch.int32)
+    kp, vp = make_pool(gen, nb, bs, h, d, dtype, cuda)
+    q, kn, vn = (torch.randn(bsz, h, d, generator=gen).to(cuda, dtype) for _ in range(3))
+
+    def run(order):
+        kpool, vpool = kp.clone(), vp.clone()
+        o = torch.as_tensor(order)
+        if trows:  # rows read table row perm[b] of a shuffled table
+            shuffle = torch.randperm(bsz, generator=torch.Generator().manual_seed(1))
+            tab = torch.empty_like(tables)
+            tab[shuffle] = tables
+            rows = shuffle[o].to(torch.int32).to(cuda)
+            out = native.paged_attention(q[o.to(cuda)], kpool, vpool, tab.to(cuda), ctx[o].to(torch.int32).to(cuda),
+                                         max_ctx, 0.125, table_rows=rows, k_new=kn[o.to(cuda)], v_new=vn[o.to(cuda)])
+        else:
+            out = native.paged_attention(q[o.to(cuda)], kpool, vpool, tables[o].to(cuda),
+                                         ctx[o].to(torch.int32).to(cuda), max_ctx, 0.125, k_new=kn[o.to(cuda)],
+                                         v_new=vn[o.to(cuda)])
+        torch.cuda.synchronize()
+        back = torch.empty_like(out)
+        back[o.to(cuda)] = out
+        return back, kpool, vpool
+
+    longest_first = sorted(range(bsz), key=lambda i: (-int(ctx[i]), i))
+    drawn = torch.randperm(bsz, generator=gen).tolist()
+    shortest_first = longest_first[::-1]
+    ref_out, ref_k, ref_v = run(longest_first)
+    for order in (list(range(bsz)), drawn, shortest_first):
+        out, k2, v2 = run(order)
+        assert torch.equal(out, ref_out)
+        assert torch.equal(k2, ref_k) and torch.equal(v2, ref_v)
+    want = O.paged_attention(f64(q)[:, None], f64(ref_k), f64(ref_v), tables.numpy(), ctx.tolist(), 0.125)[:, 0]
+    err = assert_close(ref_out, want, dtype, f"rows in any order, batch {bsz}")
+    print(f"rows in any order, batch {bsz}, ties {ties}, table rows {trows}: bit-equal in 4 orders, max err {err:.2e}")
