@@ -283,19 +283,26 @@ def large_v3_kernels(torch, native, dev, a):
     """Fused paged attention and cross-attention at Whisper-large-v3 decoder shapes, batch 64, bf16."""
     dt, b, h, d = torch.bfloat16, 64, 20, 64
     out = {}
-    for sorted_rows in (True, False):
+    # Rows longest-first with SKV_ATTN_ROWS_LONGEST_FIRST (the graph decode's layout), the same rows
+    # without the flag (the launch checks their order itself), and rows in drawn order (ranked in the launch).
+    for sorted_rows, flag in ((True, True), (True, False), (False, False)):
         sets = paged_sets(torch, native, dev, dt, b, h, d, 16, 4096, 452, a.seed + 100, 0, sorted_rows)
         fns = [lambda s=s: native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, 0.125,
-                                                  out=s.out, k_new=s.k_new, v_new=s.v_new) for s in sets]
+                                                  out=s.out, k_new=s.k_new, v_new=s.v_new, rows_longest_first=flag)
+               for s in sets]
         avg = graph_launch_us(torch, fns)
         byts = sum(s.bytes for s in sets) / len(sets)
-        if sorted_rows:
+        if flag:
             out["large_v3_paged_attention"] = {
                 "shape": "bf16, 20 heads x 64, batch 64, block size 16, ctx U[1,452], fused append, "
-                         "rows longest-first",
+                         "rows longest-first (flagged SKV_ATTN_ROWS_LONGEST_FIRST, as the graph decode does)",
                 "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
                 "achieved_GBps": round(byts / (avg * 1e-6) / 1e9, 1),
                 "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        elif sorted_rows:
+            r = out["large_v3_paged_attention"]
+            r["longest_first_unflagged_avg_launch_us"] = round(avg, 3)
+            r["longest_first_unflagged_frac"] = round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
         else:
             r = out["large_v3_paged_attention"]
             r["unsorted_rows_avg_launch_us"] = round(avg, 3)
@@ -305,7 +312,8 @@ def large_v3_kernels(torch, native, dev, a):
     # The same kernel at batch 128 (the large-v3 serving configuration's slot count).
     sets = paged_sets(torch, native, dev, dt, 128, h, d, 16, 4096, 452, a.seed + 150, 0, True)
     fns = [lambda s=s: native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, 0.125,
-                                              out=s.out, k_new=s.k_new, v_new=s.v_new) for s in sets]
+                                              out=s.out, k_new=s.k_new, v_new=s.v_new, rows_longest_first=True)
+           for s in sets]
     avg = graph_launch_us(torch, fns)
     byts = sum(s.bytes for s in sets) / len(sets)
     out["large_v3_paged_attention"]["batch128"] = {
@@ -853,9 +861,9 @@ def main():
                       a.max_ctx, a.seed, a.chunk)
     nsets = len(sets)
 
-    def step(s):
+    def step(s, longest_first=True):
         native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, a.max_ctx, scale, out=s.out,
-                               chunk_tokens=a.chunk, k_new=s.k_new, v_new=s.v_new)
+                               chunk_tokens=a.chunk, k_new=s.k_new, v_new=s.v_new, rows_longest_first=longest_first)
 
     # Steps run as captured graphs of back-to-back launches, as the decode runs them: graphs[n]
     # holds the steps of sets 0..n-1 in order, so K steps are K // nsets replays of the full
@@ -895,6 +903,8 @@ def main():
     avg_us = graph_launch_us(torch, [lambda s=s: step(s) for s in sets])
     avg_bytes = sum(s.bytes for s in sets) / nsets
     achieved = avg_bytes / (avg_us * 1e-6) / 1e9
+    # The same longest-first rows without the flag: the launch checks their order itself.
+    unflagged_us = graph_launch_us(torch, [lambda s=s: step(s, False) for s in sets])
 
     # Correctness guard on the measured data: one set against the oracle.
     import numpy as np
@@ -933,7 +943,7 @@ def main():
             "max_ctx": a.max_ctx,
             "rotating_sets": nsets,
             "step_launch": f"captured graphs of {nsets} back-to-back steps (one per set), as the decode replays them",
-            "rows": "longest-first (the engine's decode batch layout)",
+            "rows": "longest-first, flagged SKV_ATTN_ROWS_LONGEST_FIRST (the graph decode's batch layout)",
             "chunk_tokens": a.chunk or native.default_chunk_tokens(a.batch, a.heads, a.head_dim, a.max_ctx, dtype),
             "library": native.version(),
         },
@@ -960,7 +970,10 @@ def main():
     # The same workload with the rows in drawn order, for comparison.
     sets = paged_sets(torch, native, dev, dtype, a.batch, a.heads, a.head_dim, a.block_size, a.pool_blocks,
                       a.max_ctx, a.seed, a.chunk, sorted_rows=False)
-    un_us = graph_launch_us(torch, [lambda s=s: step(s) for s in sets])
+    un_us = graph_launch_us(torch, [lambda s=s: step(s, False) for s in sets])
+    result["roofline"]["longest_first_unflagged_avg_launch_us"] = round(unflagged_us, 3)
+    result["roofline"]["longest_first_unflagged_frac"] = round(avg_bytes / (unflagged_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                                               4)
     result["roofline"]["unsorted_rows_avg_launch_us"] = round(un_us, 3)
     result["roofline"]["unsorted_rows_frac"] = round(sum(s.bytes for s in sets) / len(sets) / (un_us * 1e-6) / 1e9
                                                      / HBM_PEAK_GBS, 4)

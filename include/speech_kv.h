@@ -73,6 +73,13 @@ extern "C" {
 
 enum skv_dtype { SKV_F32 = 0, SKV_F16 = 1, SKV_BF16 = 2 };
 
+/* Bits of the attention entry points' `causal` argument (0 / 1 keep their meaning). */
+enum skv_attn_flags {
+  SKV_ATTN_CAUSAL = 1,             /* query qi sees ctx_lens[b] - (q_len - 1 - qi) keys */
+  SKV_ATTN_ROWS_LONGEST_FIRST = 2  /* skv_paged_attention: the rows come in non-increasing ctx_lens
+                                      order, so the launch need not rank them itself */
+};
+
 enum skv_status {
   SKV_OK = 0,
   SKV_EINVAL = -1,     /* bad size / null pointer / unsupported head_dim */
@@ -205,8 +212,9 @@ SKV_API int32_t skv_paged_chunk_tokens(int32_t rows, int32_t num_heads, int32_t 
  *   block_tables   : int32 [*, table_stride]; row b uses table row
  *                    table_rows ? table_rows[b] : b
  *   ctx_lens : int32 [B] keys visible to the LAST query of row b (new token
- *              included). With causal != 0, query qi sees ctx_lens[b] - (Q-1-qi)
- *              keys; otherwise every query sees ctx_lens[b].
+ *              included). With SKV_ATTN_CAUSAL in `causal`, query qi sees
+ *              ctx_lens[b] - (Q-1-qi) keys; otherwise every query sees ctx_lens[b].
+ *   causal   : SKV_ATTN_CAUSAL | SKV_ATTN_ROWS_LONGEST_FIRST bits (skv_attn_flags).
  *   max_ctx  : upper bound of ctx_lens (sizes the launch grid).
  *   k_new, v_new (optional, both or neither): [B, Q, num_kv_heads, D] rows of
  *              the Q newest keys of each row, i.e. positions
@@ -221,11 +229,14 @@ SKV_API int32_t skv_paged_chunk_tokens(int32_t rows, int32_t num_heads, int32_t 
  * queries per row and (row, head, 64-query) workgroups for at least three quarters
  * of the GPU's compute units, every 64 queries share one read of the blocks staged
  * in LDS.
- * Row order: the launch spreads (row, head) items over the compute units in a fixed
- * order that balances their bytes when rows come longest-first (as the scheduler lays
- * out its decode batch); rows in arbitrary order give correct results but an uneven
- * per-unit load (Whisper-large-v3 shape, batch 64: 14.5 us longest-first, 17.6 us in
- * random order).
+ * Row order: the launch spreads (row, head) items over the compute units in an order that
+ * balances their bytes when the items go longest row first. A decode launch (q_len 1, one
+ * key chunk per row, at most 64 rows) ranks its rows by length class itself (the top 4
+ * bits of the length), so rows may come in any order; results do not depend on the order.
+ * A caller whose rows already come longest-first (as the graph decode lays out its batch)
+ * sets SKV_ATTN_ROWS_LONGEST_FIRST in `causal` to skip the ranking (Whisper-large-v3 shape,
+ * batch 64: 14.5 us with the flag, 14.9 us without it, 15.2 us for rows in random order,
+ * against 17.5 us for random order without any ranking).
  * Reference: models.py:126-165, :444-466; scripts/evaluate_paging_variants.py:56-133.
  */
 SKV_API int skv_paged_attention(const void* q, int64_t q_stride_b, int64_t q_stride_q, int64_t q_stride_h,

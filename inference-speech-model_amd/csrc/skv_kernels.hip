@@ -647,6 +647,7 @@ constexpr int kPartPad = 4;             // partial record = m, l, pad, pad, acc[
 // s_waitcnt immediate for vmcnt(0) alone (expcnt and lgkmcnt at their maxima).
 constexpr int kWaitVmcnt0 = 0x0f70;
 constexpr int kRankRows = 64;  // most rows a launch ranks by length (one per lane of a wave)
+constexpr int kRankBits = 4;   // length bits the ranking orders by (16 length classes)
 
 struct AttnParams {
   const uint4* q;  // strides below are in 16-byte vector units
@@ -876,13 +877,14 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
     h = (int)item - row * heads;
     chunk = 0;
     if constexpr (PAGED) {
-      // Rank order: `row` is a rank, and the workgroup takes the row whose length has that rank
-      // (longest first, ties to the lower row). Every wave reads the lengths, one row per lane,
-      // with a buffer load (lanes past the batch read zero; the batch is items / heads, exact as
-      // for the row above). Rows already longest-first need nothing more: the rank is the row.
-      // Otherwise wave 0 selects the row, a radix selection over the length bits with wave
-      // ballots and then the rank's place among equal lengths, and hands it to the other waves
-      // through LDS.
+      // Rank order: `row` is a rank, and the workgroup takes the row of that rank in the order of
+      // the rows' length classes (the top kRankBits bits of the length below 2^bitlen(max_len):
+      // longest first, ties to the lower row), which balances the units' bytes as well as an
+      // exact sort to within one class. Every wave reads the lengths, one row per lane, with a
+      // buffer load (lanes past the batch read zero; the batch is items / heads, exact as for the
+      // row above). Rows already longest-first need nothing more: the rank is the row. Otherwise
+      // wave 0 selects the row, a radix selection over the class bits with wave ballots and then
+      // the rank's place within its class, and hands it to the other waves through LDS.
       if (flags & 8u) {
         const uint32_t nrows = __umulhi(items, heads_magic);
         const __amdgpu_buffer_rsrc_t lres = __builtin_amdgcn_make_buffer_rsrc(
@@ -898,7 +900,8 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
           if (__builtin_amdgcn_readfirstlane(wave) == 0) {
             uint64_t cand = __ballot((uint32_t)lane < nrows);
             uint32_t k = (uint32_t)row;
-            for (int bit = 31 - __clz(max(max_len, 1)); bit >= 0; --bit) {
+            const int top = 31 - __clz(max(max_len, 1));
+            for (int bit = top; bit >= max(top + 1 - kRankBits, 0); --bit) {
               const uint64_t ones = __ballot((lenj >> bit) & 1) & cand;
               const uint32_t c = (uint32_t)__popcll(ones);
               if (k < c) {
@@ -908,7 +911,7 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
                 cand &= ~ones;
               }
             }
-            for (; k > 0; --k) cand &= cand - 1;  // the k-th lowest row of the remaining length
+            for (; k > 0; --k) cand &= cand - 1;  // the k-th lowest row of the remaining class
             if (lane == 0) s_ranked_row = __ffsll((unsigned long long)cand) - 1;
           }
           lds_barrier();
@@ -2639,6 +2642,10 @@ int paged_attention_impl(const char* who, const void* q, int64_t q_stride_b, int
                          int32_t num_blocks, int32_t max_ctx, float scale, int32_t causal, int32_t dtype,
                          int32_t chunk_tokens, void* workspace, int64_t ws_bytes, bool fixed_scratch,
                          void* stream) {
+  // causal is a flags word: SKV_ATTN_CAUSAL, and SKV_ATTN_ROWS_LONGEST_FIRST when the caller's rows
+  // already come longest-first (the launch then keeps their order instead of ranking them).
+  const bool longest_first = (causal & SKV_ATTN_ROWS_LONGEST_FIRST) != 0;
+  causal &= SKV_ATTN_CAUSAL;
   if (block_size < 2 || num_blocks < 0 || table_stride <= 0 || !block_tables)
     return fail(SKV_EINVAL, "%s: bad block table arguments (block_size must be >= 2)", who);
   if ((k_new == nullptr) != (v_new == nullptr))
@@ -2690,7 +2697,7 @@ int paged_attention_impl(const char* who, const void* q, int64_t q_stride_b, int
     p.nchunk_max = 1;
     p.snake = 0;
   }
-  p.rank = p.snake && q_len == 1 && batch <= kRankRows;
+  p.rank = p.snake && q_len == 1 && batch <= kRankRows && !longest_first;
   rc = bind_workspace(p, who, head_dim, workspace, ws_bytes);
   if (rc != SKV_OK) {
     if (!fixed_scratch) return rc;

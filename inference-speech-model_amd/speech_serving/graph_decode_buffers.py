@@ -257,7 +257,9 @@ class GraphDecodeBuffers:
         rows = self.g_rows[:, :bucket]
         row_slot, ctx, enc, cslot = rows[0], rows[1], rows[2], rows[3]
         ids = self.g_slot_tokens.index_select(0, row_slot).view(bucket, 1)
-        kv = PagedKV(self.bm.key_pool, self.bm.value_pool, self.g_tables, ctx, self.max_ctx, table_rows=row_slot)
+        # prepare_replay lays the rows out longest-first (idle rows, of length 0, last)
+        kv = PagedKV(self.bm.key_pool, self.bm.value_pool, self.g_tables, ctx, self.max_ctx, table_rows=row_slot,
+                     rows_longest_first=True)
         cross = CrossKV([self.g_cross_kv[:, l, 0] for l in range(self.num_decoder_layers)],
                         [self.g_cross_kv[:, l, 1] for l in range(self.num_decoder_layers)],
                         enc, self.max_enc_len, slot_ids=cslot)

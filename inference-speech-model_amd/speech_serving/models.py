@@ -88,6 +88,7 @@ class PagedKV:
     ctx_lens: torch.Tensor
     max_ctx: int
     table_rows: Optional[torch.Tensor] = None
+    rows_longest_first: bool = False  # rows in non-increasing ctx_lens order (the launch need not rank them)
 
 
 class _GatheredLayer:
@@ -324,7 +325,7 @@ class DecoderLayer(nn.Module):
         q, k, v = self._qkv_normed(h)
         attn = native.paged_attention(q, kv.k_pools[layer], kv.v_pools[layer], kv.block_tables, kv.ctx_lens,
                                       kv.max_ctx, self.scale, causal=s > 1, table_rows=kv.table_rows,
-                                      k_new=k, v_new=v)
+                                      k_new=k, v_new=v, rows_longest_first=kv.rows_longest_first)
         a = self.self_attn_out(attn.view(b, s, hd))
         used = cross is not None and cross.has(layer)
         if used:

@@ -24,6 +24,7 @@ _lib: Optional[ctypes.CDLL] = None
 _lib_lock = threading.Lock()
 
 SKV_F32, SKV_F16, SKV_BF16 = 0, 1, 2
+SKV_ATTN_CAUSAL, SKV_ATTN_ROWS_LONGEST_FIRST = 1, 2  # bits of the attention calls' `causal`
 _DTYPE_CODE = {torch.float32: SKV_F32, torch.float16: SKV_F16, torch.bfloat16: SKV_BF16}
 
 # Exported entry points and their ctypes signatures (must match include/speech_kv.h).
@@ -423,7 +424,8 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                     ctx_lens: torch.Tensor, max_ctx: int, scale: float, causal: bool = False,
                     table_rows: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
                     chunk_tokens: int = 0, k_new: Optional[torch.Tensor] = None,
-                    v_new: Optional[torch.Tensor] = None, noalloc: bool = False) -> torch.Tensor:
+                    v_new: Optional[torch.Tensor] = None, noalloc: bool = False,
+                    rows_longest_first: bool = False) -> torch.Tensor:
     """softmax(q K^T * scale) V over each row's paged K/V.
 
     q: [B, H, D] or [B, Q, H, D]; pools [num_blocks, BS, Hkv, D]; block_tables
@@ -434,6 +436,8 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     through the block table in the same launch.
     With noalloc the call goes through skv_paged_attention_noalloc: split-K partials in the library's
     fixed per-device scratch (at most 4 MiB), no workspace; pass `out` to allocate nothing at all.
+    rows_longest_first: the rows come in non-increasing ctx_lens order (the launch then skips ranking
+    them by length; results are the same either way).
     Reference math: speech_serving/models.py:126-165 and :444-466; append:
     speech_serving/phase_aware_scheduler.py:1004-1010.
     """
@@ -486,7 +490,8 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
             block_tables.data_ptr(), block_tables.stride(0), _ptr(table_rows), ctx_lens.data_ptr(),
             _ptr(kn4), _ptr(vn4), nstr[0], nstr[1], nstr[2],
             o4.data_ptr(), o4.stride(0), o4.stride(1), o4.stride(2), bsz, qlen, heads, hkv, d, bs, nb, max_ctx,
-            float(scale), 1 if causal else 0, code, chunk_tokens)
+            float(scale), (SKV_ATTN_CAUSAL if causal else 0) | (SKV_ATTN_ROWS_LONGEST_FIRST if rows_longest_first else 0),
+            code, chunk_tokens)
     if noalloc:
         _check(lib().skv_paged_attention_noalloc(*args, _stream(q.device)), "skv_paged_attention_noalloc")
         return out

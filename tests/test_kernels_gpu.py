@@ -411,10 +411,10 @@ def test_graph_replay_matches_eager(cuda):
 @pytest.mark.parametrize("bsz,ties,trows", [(64, False, False), (64, True, False), (63, False, True), (65, False, False),
                                             (20, True, True), (1, False, False)])
 def test_paged_attention_rows_in_any_order(cuda, bsz, ties, trows):
-    """A launch of up to 64 decode rows takes its (row, head) items in length order whatever order the rows
-    come in (more rows keep the given order): the same rows in any order give, row for row, the same bits
-    (outputs and appended pool rows), within the oracle bar. Ties: lengths from a few values; rows past the
-    table's reach clamp to it."""
+    """A launch of up to 64 decode rows takes its (row, head) items in length-class order whatever order the
+    rows come in (more rows, or rows flagged longest-first, keep the given order): the same rows in any order,
+    flagged or not, give row for row the same bits (outputs and appended pool rows), within the oracle bar.
+    Ties: lengths from a few values."""
     gen = torch.Generator().manual_seed(700 + bsz + 2 * ties + trows)
     h, d, bs, dtype, max_ctx = 20, 64, 16, torch.bfloat16, 452
     maxblk = -(-max_ctx // bs)
@@ -427,7 +427,7 @@ def test_paged_attention_rows_in_any_order(cuda, bsz, ties, trows):
     kp, vp = make_pool(gen, nb, bs, h, d, dtype, cuda)
     q, kn, vn = (torch.randn(bsz, h, d, generator=gen).to(cuda, dtype) for _ in range(3))
 
-    def run(order):
+    def run(order, longest_first=False):
         kpool, vpool = kp.clone(), vp.clone()
         o = torch.as_tensor(order)
         if trows:  # rows read table row perm[b] of a shuffled table
@@ -436,11 +436,12 @@ def test_paged_attention_rows_in_any_order(cuda, bsz, ties, trows):
             tab[shuffle] = tables
             rows = shuffle[o].to(torch.int32).to(cuda)
             out = native.paged_attention(q[o.to(cuda)], kpool, vpool, tab.to(cuda), ctx[o].to(torch.int32).to(cuda),
-                                         max_ctx, 0.125, table_rows=rows, k_new=kn[o.to(cuda)], v_new=vn[o.to(cuda)])
+                                         max_ctx, 0.125, table_rows=rows, k_new=kn[o.to(cuda)], v_new=vn[o.to(cuda)],
+                                         rows_longest_first=longest_first)
         else:
             out = native.paged_attention(q[o.to(cuda)], kpool, vpool, tables[o].to(cuda),
                                          ctx[o].to(torch.int32).to(cuda), max_ctx, 0.125, k_new=kn[o.to(cuda)],
-                                         v_new=vn[o.to(cuda)])
+                                         v_new=vn[o.to(cuda)], rows_longest_first=longest_first)
         torch.cuda.synchronize()
         back = torch.empty_like(out)
         back[o.to(cuda)] = out
@@ -450,10 +451,13 @@ def test_paged_attention_rows_in_any_order(cuda, bsz, ties, trows):
     drawn = torch.randperm(bsz, generator=gen).tolist()
     shortest_first = longest_first[::-1]
     ref_out, ref_k, ref_v = run(longest_first)
-    for order in (list(range(bsz)), drawn, shortest_first):
-        out, k2, v2 = run(order)
+    # with the longest-first flag (rows in that order, and, wrongly, in drawn order: only the work's
+    # placement may change) and without it
+    for order, flag in ((longest_first, True), (drawn, True), (list(range(bsz)), False), (drawn, False),
+                        (shortest_first, False)):
+        out, k2, v2 = run(order, flag)
         assert torch.equal(out, ref_out)
         assert torch.equal(k2, ref_k) and torch.equal(v2, ref_v)
     want = O.paged_attention(f64(q)[:, None], f64(ref_k), f64(ref_v), tables.numpy(), ctx.tolist(), 0.125)[:, 0]
     err = assert_close(ref_out, want, dtype, f"rows in any order, batch {bsz}")
-    print(f"rows in any order, batch {bsz}, ties {ties}, table rows {trows}: bit-equal in 4 orders, max err {err:.2e}")
+    print(f"rows in any order, batch {bsz}, ties {ties}, table rows {trows}: bit-equal in 6 runs, max err {err:.2e}")
