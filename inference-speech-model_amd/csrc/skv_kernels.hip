@@ -214,6 +214,73 @@ __global__ __launch_bounds__(256) void gather_kernel(const uint4* __restrict__ k
   }
 }
 
+// Gather by waves (a power-of-two block size of at least 64 / vpr keys, a pool of at
+// most 2 GiB): one wave copies kGatherLoads * 64 / vpr consecutive token rows of one
+// (row, head), 64 / vpr rows per load instruction (vpr lanes per row). The rows of
+// one instruction lie in one block, so its block id is wave-uniform: the row length
+// and the instructions' block ids (their table index clamped to the row) load in one
+// scalar batch, and the pool loads follow after that single round trip. Pool rows
+// are read with buffer loads against a descriptor of the pool; a row at or past the
+// length, or behind a block id outside the pool, gets an out-of-range offset, for
+// which the hardware returns zeros without a memory access, so the padding costs no
+// read and no load is predicated. Output rows past T (the last group) are not stored.
+// The arguments of the address chain come first, as plain scalars (the divisors'
+// fields apart: preloading stops at an aggregate): the build preloads the first
+// argument dwords into scalar registers, so the chain starts without an argument load.
+constexpr int kGatherLoads = 4;
+__global__ __launch_bounds__(256) void gather_rows_kernel(uint32_t waves, uint32_t row_d, uint32_t row_m,
+                                                          uint32_t head_d, uint32_t head_m, int32_t tstride,
+                                                          int32_t bs_shift, int32_t vpr_shift,
+                                                          const int32_t* __restrict__ tables,
+                                                          const int32_t* __restrict__ lens, int32_t T, int32_t nb,
+                                                          int32_t heads, uint32_t pool_bytes,
+                                                          const uint4* __restrict__ k_pool,
+                                                          const uint4* __restrict__ v_pool, uint4* __restrict__ k_out,
+                                                          uint4* __restrict__ v_out) {
+  const uint32_t w = blockIdx.x * 4u + (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (w >= waves) return;
+  const DivU32 per_row{row_d, row_m}, per_head{head_d, head_m};
+  const uint4* src = blockIdx.y == 0 ? k_pool : v_pool;
+  uint4* dst = blockIdx.y == 0 ? k_out : v_out;
+  const int lane = threadIdx.x & 63;
+  const uint32_t b = udiv(w, per_row);
+  const uint32_t r = w - b * per_row.d;
+  const uint32_t h = udiv(r, per_head);
+  const uint32_t grp = r - h * per_head.d;
+  const int rpi = 64 >> vpr_shift;  // rows per load instruction
+  const int t0 = (int)grp * rpi * kGatherLoads;
+  const int32_t* trow = tables + (int64_t)b * tstride;
+  int len = lens[b];
+  uint32_t blk[kGatherLoads];
+#pragma unroll
+  for (int u = 0; u < kGatherLoads; ++u) blk[u] = (uint32_t)trow[min((t0 + u * rpi) >> bs_shift, tstride - 1)];
+  asm volatile("" ::"s"(len), "s"(blk[0]), "s"(blk[1]), "s"(blk[2]), "s"(blk[3]));
+  const int64_t lim = (int64_t)tstride << bs_shift;
+  len = len < 0 ? 0 : (len > T ? T : len);
+  len = (int64_t)len < lim ? len : (int)lim;
+  const uint32_t row_bytes = ((uint32_t)heads << vpr_shift) * 16u;  // one token row of every head
+  const int row = lane >> vpr_shift;
+  const uint32_t col = ((h << vpr_shift) + (uint32_t)(lane & ((1 << vpr_shift) - 1))) * 16u;
+  const __amdgpu_buffer_rsrc_t res =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(src), (short)0, (int)pool_bytes, kBufWord3);
+  const uint32_t bmask = (1u << bs_shift) - 1u;
+  uint4 val[kGatherLoads];
+#pragma unroll
+  for (int u = 0; u < kGatherLoads; ++u) {
+    const int t = t0 + u * rpi + row;
+    const uint32_t off = t < len && blk[u] < (uint32_t)nb
+                             ? ((blk[u] << bs_shift) + ((uint32_t)t & bmask)) * row_bytes + col
+                             : kBufOutOfRange;
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(res, off, 0, kBufNt);
+    val[u] = make_uint4(x.x, x.y, x.z, x.w);
+  }
+  const uint32_t o = ((b * (uint32_t)heads + h) * (uint32_t)T + (uint32_t)t0 + (uint32_t)row) << vpr_shift |
+                     (uint32_t)(lane & ((1 << vpr_shift) - 1));
+#pragma unroll
+  for (int u = 0; u < kGatherLoads; ++u)
+    if (t0 + u * rpi + row < T) dst[o + ((uint32_t)(u * rpi) << vpr_shift)] = val[u];
+}
+
 // ---------------------------------------------------------------------------
 // Encoder K/V into a decode slot: for every (layer, K|V) source and head h the
 // first n positions (rows of D elements) are copied into the slot's region of
@@ -2432,6 +2499,22 @@ int skv_gather(const void* k_pool, const void* v_pool, const int32_t* block_tabl
   const int64_t total = (int64_t)batch * num_heads * max_len * vpr;
   int64_t blocks = cdiv(total, 256);
   if (blocks > 65535) blocks = 65535;
+  const bool pow2 = (block_size & (block_size - 1)) == 0 && (vpr & (vpr - 1)) == 0;
+  const int64_t pool_bytes = (int64_t)num_blocks * block_size * num_heads * vpr * 16;
+  if (pow2 && vpr <= 64 && 64 / vpr <= block_size && table_stride >= 1 && pool_bytes <= kBufLimit &&
+      total < ((int64_t)1 << 31)) {
+    const int64_t groups = cdiv(max_len, (int64_t)(64 / vpr) * kGatherLoads);
+    const int64_t waves = (int64_t)batch * num_heads * groups;
+    if (waves > 0 && cdiv(waves, 4) <= 0x7fffffff) {
+      const DivU32 per_row = make_div((uint32_t)(num_heads * groups)), per_head = make_div((uint32_t)groups);
+      hipLaunchKernelGGL(gather_rows_kernel, dim3((uint32_t)cdiv(waves, 4), v_pool ? 2 : 1), dim3(256), 0,
+                         (hipStream_t)stream, (uint32_t)waves, per_row.d, per_row.m, per_head.d, per_head.m,
+                         table_stride, __builtin_ctz((unsigned)block_size), __builtin_ctz((unsigned)vpr),
+                         block_tables, lens, max_len, num_blocks, num_heads, (uint32_t)pool_bytes, (const uint4*)k_pool, (const uint4*)(v_pool ? v_pool : k_pool),
+                         (uint4*)k_out, (uint4*)(v_out ? v_out : k_out));
+      return check_launch("skv_gather");
+    }
+  }
   if (total < ((int64_t)1 << 31)) {
     const uint32_t per_head = (uint32_t)cdiv(max_len, kGatherRows) * (uint32_t)vpr;
     const int64_t groups = (int64_t)batch * num_heads * per_head;
