@@ -713,7 +713,7 @@ constexpr int kMaxChunkBlocks = 256;    // LDS block-id slots per chunk
 constexpr int kPartPad = 4;             // partial record = m, l, pad, pad, acc[D]
 // s_waitcnt immediate for vmcnt(0) alone (expcnt and lgkmcnt at their maxima).
 constexpr int kWaitVmcnt0 = 0x0f70;
-constexpr int kRankRows = 64;  // most rows a launch ranks by length (one per lane of a wave)
+constexpr int kRankRows = 128;  // most rows a launch ranks by length (one or two per lane of a wave)
 constexpr int kRankBits = 4;   // length bits the ranking orders by (16 length classes)
 
 struct AttnParams {
@@ -947,11 +947,13 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
       // Rank order: `row` is a rank, and the workgroup takes the row of that rank in the order of
       // the rows' length classes (the top kRankBits bits of the length below 2^bitlen(max_len):
       // longest first, ties to the lower row), which balances the units' bytes as well as an
-      // exact sort to within one class. Every wave reads the lengths, one row per lane, with a
+      // exact sort to within one class. Every wave reads the lengths, one row per lane with a
       // buffer load (lanes past the batch read zero; the batch is items / heads, exact as for the
-      // row above). Rows already longest-first need nothing more: the rank is the row. Otherwise
-      // wave 0 selects the row, a radix selection over the class bits with wave ballots and then
-      // the rank's place within its class, and hands it to the other waves through LDS.
+      // row above), and rows 64-127 with a second load when the batch has them. Rows already
+      // longest-first need nothing more: the rank is the row. Otherwise wave 0 selects the row, a
+      // radix selection over the class bits with wave ballots and then the rank's place within
+      // its class, and hands it to the other waves through LDS. Batches of up to 64 rows take a
+      // copy of this code without the second half.
       if (flags & 8u) {
         const uint32_t nrows = __umulhi(items, heads_magic);
         const __amdgpu_buffer_rsrc_t lres = __builtin_amdgcn_make_buffer_rsrc(
@@ -962,29 +964,64 @@ __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PAG
                      "s"(p.k), "s"(p.v), "s"(p.nb), "s"(p.row_vecs), "s"(p.kv_bytes), "s"(p.kn), "s"(p.vn),
                      "s"(p.nsb), "s"(p.nsh), "s"(p.nchunk_max));
         const int lenj = min(max(lraw, 0), max_len);
-        const int prev = __shfl_up(lenj, 1);
-        if (__any(lane > 0 && lenj > prev)) {  // the same in every wave (lanes past the batch hold 0)
-          if (__builtin_amdgcn_readfirstlane(wave) == 0) {
-            uint64_t cand = __ballot((uint32_t)lane < nrows);
-            uint32_t k = (uint32_t)row;
-            const int top = 31 - __clz(max(max_len, 1));
-            for (int bit = top; bit >= max(top + 1 - kRankBits, 0); --bit) {
-              const uint64_t ones = __ballot((lenj >> bit) & 1) & cand;
-              const uint32_t c = (uint32_t)__popcll(ones);
-              if (k < c) {
-                cand = ones;
-              } else {
-                k -= c;
-                cand &= ~ones;
-              }
-            }
-            for (; k > 0; --k) cand &= cand - 1;  // the k-th lowest row of the remaining class
-            if (lane == 0) s_ranked_row = __ffsll((unsigned long long)cand) - 1;
+        auto rank = [&](auto two_c) __attribute__((always_inline)) {
+          constexpr bool TWO = decltype(two_c)::value;  // rows 64-127 in a second register
+          int lraw1 = 0, lenj1 = 0;
+          if constexpr (TWO) {
+            lraw1 = (int)__builtin_amdgcn_raw_buffer_load_b32(lres, (uint32_t)(lane + 64) * 4u, 0, 0);
+            lenj1 = min(max(lraw1, 0), max_len);
           }
-          lds_barrier();
-          row = __builtin_amdgcn_readfirstlane(s_ranked_row);
-        }
-        ranked_len = __builtin_amdgcn_readlane(lraw, row);
+          const int prev = __shfl_up(lenj, 1);
+          bool rises = lane > 0 && lenj > prev;  // the same in every wave (rows past the batch hold 0)
+          if constexpr (TWO) {
+            const int prev1 = __shfl_up(lenj1, 1);
+            rises = rises || lenj1 > (lane == 0 ? __builtin_amdgcn_readlane(lenj, 63) : prev1);
+          }
+          if (__any(rises)) {
+            if (__builtin_amdgcn_readfirstlane(wave) == 0) {
+              uint64_t cand = __ballot((uint32_t)lane < nrows), cand1 = 0;
+              if constexpr (TWO) cand1 = __ballot((uint32_t)lane + 64u < nrows);
+              uint32_t k = (uint32_t)row;
+              const int top = 31 - __clz(max(max_len, 1));
+              for (int bit = top; bit >= max(top + 1 - kRankBits, 0); --bit) {
+                const uint64_t ones = __ballot((lenj >> bit) & 1) & cand;
+                uint64_t ones1 = 0;
+                if constexpr (TWO) ones1 = __ballot((lenj1 >> bit) & 1) & cand1;
+                const uint32_t c = (uint32_t)(__popcll(ones) + (TWO ? __popcll(ones1) : 0));
+                if (k < c) {
+                  cand = ones;
+                  cand1 = ones1;
+                } else {
+                  k -= c;
+                  cand &= ~ones;
+                  cand1 &= ~ones1;
+                }
+              }
+              // the k-th lowest row of the remaining class: rows 0-63 in cand, 64-127 in cand1
+              int first = 0;
+              if constexpr (TWO) {
+                const uint32_t c0 = (uint32_t)__popcll(cand);
+                if (k >= c0) {
+                  k -= c0;
+                  cand = cand1;
+                  first = 64;
+                }
+              }
+              for (; k > 0; --k) cand &= cand - 1;
+              if (lane == 0) s_ranked_row = first + __ffsll((unsigned long long)cand) - 1;
+            }
+            lds_barrier();
+            row = __builtin_amdgcn_readfirstlane(s_ranked_row);
+          }
+          if constexpr (TWO)
+            ranked_len = row < 64 ? __builtin_amdgcn_readlane(lraw, row) : __builtin_amdgcn_readlane(lraw1, row - 64);
+          else
+            ranked_len = __builtin_amdgcn_readlane(lraw, row);
+        };
+        if (nrows > 64)
+          rank(std::true_type{});
+        else
+          rank(std::false_type{});
       }
     }
   } else if (flags & 1u) {

@@ -409,12 +409,13 @@ def test_graph_replay_matches_eager(cuda):
 
 # ------------------------------------------------------------------ row order
 @pytest.mark.parametrize("bsz,ties,trows", [(64, False, False), (64, True, False), (63, False, True), (65, False, False),
-                                            (20, True, True), (1, False, False)])
+                                            (20, True, True), (1, False, False), (128, False, False),
+                                            (100, True, True), (129, False, False)])
 def test_paged_attention_rows_in_any_order(cuda, bsz, ties, trows):
-    """A launch of up to 64 decode rows takes its (row, head) items in length-class order whatever order the
-    rows come in (more rows, or rows flagged longest-first, keep the given order): the same rows in any order,
-    flagged or not, give row for row the same bits (outputs and appended pool rows), within the oracle bar.
-    Ties: lengths from a few values."""
+    """A launch of up to 128 decode rows takes its (row, head) items in length-class order whatever order the
+    rows come in (rows 0-63 from one lane each, rows 64-127 from a second load; more rows, or rows flagged
+    longest-first, keep the given order): the same rows in any order, flagged or not, give row for row the
+    same bits (outputs and appended pool rows), within the oracle bar. Ties: lengths from a few values."""
     gen = torch.Generator().manual_seed(700 + bsz + 2 * ties + trows)
     h, d, bs, dtype, max_ctx = 20, 64, 16, torch.bfloat16, 452
     maxblk = -(-max_ctx // bs)
