@@ -309,18 +309,26 @@ def large_v3_kernels(torch, native, dev, a):
             r["unsorted_rows_frac"] = round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
         del sets, fns
         torch.cuda.empty_cache()
-    # The same kernel at batch 128 (the large-v3 serving configuration's slot count).
-    sets = paged_sets(torch, native, dev, dt, 128, h, d, 16, 4096, 452, a.seed + 150, 0, True)
-    fns = [lambda s=s: native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, 0.125,
-                                              out=s.out, k_new=s.k_new, v_new=s.v_new, rows_longest_first=True)
-           for s in sets]
-    avg = graph_launch_us(torch, fns)
-    byts = sum(s.bytes for s in sets) / len(sets)
-    out["large_v3_paged_attention"]["batch128"] = {
-        "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
-        "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    del sets, fns
-    torch.cuda.empty_cache()
+    # The same kernel at batch 128 (the large-v3 serving configuration's slot count): rows longest-first
+    # (flagged), and rows in drawn order (ranked in the launch).
+    for sorted_rows in (True, False):
+        sets = paged_sets(torch, native, dev, dt, 128, h, d, 16, 4096, 452, a.seed + 150, 0, sorted_rows)
+        fns = [lambda s=s: native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, 452, 0.125,
+                                                  out=s.out, k_new=s.k_new, v_new=s.v_new,
+                                                  rows_longest_first=sorted_rows)
+               for s in sets]
+        avg = graph_launch_us(torch, fns)
+        byts = sum(s.bytes for s in sets) / len(sets)
+        if sorted_rows:
+            out["large_v3_paged_attention"]["batch128"] = {
+                "avg_launch_us": round(avg, 3), "algorithmic_bytes_per_launch": int(byts),
+                "frac": round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        else:
+            r = out["large_v3_paged_attention"]["batch128"]
+            r["unsorted_rows_avg_launch_us"] = round(avg, 3)
+            r["unsorted_rows_frac"] = round(byts / (avg * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        del sets, fns
+        torch.cuda.empty_cache()
     t = 1500
     kvs = []
     for i in range(2):  # 2 x 491 MB > 256 MB last-level cache
