@@ -175,6 +175,9 @@ class ProblemSet:
         self.bytes = attention_bytes(self.ctx.tolist(), heads, d, elt, bs) + append_write_bytes(batch, heads, d, elt)
 
 
+GRAPH_STEPS = 32  # steps per captured graph in the timed region: the large-v3 decoder's layers per token step
+
+
 def graph_launch_us(torch, fns, per_fn=8, replays=7):
     """Average duration of one launch, from HIP events around replays of a captured graph that
     holds per_fn back-to-back launches of every fn (rotating through fns). The events sit on the
@@ -873,9 +876,10 @@ def main():
         native.paged_attention(s.q, s.k_pool, s.v_pool, s.tables, s.ctx_dev, a.max_ctx, scale, out=s.out,
                                chunk_tokens=a.chunk, k_new=s.k_new, v_new=s.v_new, rows_longest_first=longest_first)
 
-    # Steps run as captured graphs of back-to-back launches, as the decode runs them: graphs[n]
-    # holds the steps of sets 0..n-1 in order, so K steps are K // nsets replays of the full
-    # rotation plus one replay of the first K mod nsets sets.
+    # Steps run as captured graphs of back-to-back launches, as the decode runs them: its graph of one
+    # token step holds one attention launch per decoder layer (32 at large-v3). graphs[n] holds n steps
+    # cycling through the sets (step j on set j mod nsets), so K steps are K // GRAPH_STEPS replays of
+    # graphs[GRAPH_STEPS] plus one replay of graphs[K mod GRAPH_STEPS].
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -883,28 +887,31 @@ def main():
             step(s)
     torch.cuda.current_stream().wait_stream(stream)
     graphs = {}
-    for n in sorted({nsets, a.steps % nsets, a.warmup % nsets} - {0}):
+    for n in sorted({GRAPH_STEPS, a.steps % GRAPH_STEPS, a.warmup % GRAPH_STEPS} - {0}):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for s in sets[:n]:
-                step(s)
+            for j in range(n):
+                step(sets[j % nsets])
         graphs[n] = g
     torch.cuda.synchronize()
 
     def run_steps(k):
-        for _ in range(k // nsets):
-            graphs[nsets].replay()
-        if k % nsets:
-            graphs[k % nsets].replay()
+        """Replays k steps; returns the algorithmic bytes they move."""
+        for _ in range(k // GRAPH_STEPS):
+            graphs[GRAPH_STEPS].replay()
+        if k % GRAPH_STEPS:
+            graphs[k % GRAPH_STEPS].replay()
+        per_graph = [sum(sets[j % nsets].bytes for j in range(n)) for n in (GRAPH_STEPS, k % GRAPH_STEPS)]
+        return (k // GRAPH_STEPS) * per_graph[0] + per_graph[1]
 
     run_steps(a.warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    run_steps(a.steps)
+    moved = run_steps(a.steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / a.steps * 1e3
-    value = sum(sets[i % nsets].bytes for i in range(a.steps)) / wall / 1e9
+    value = moved / wall / 1e9
 
     # Roofline of the dominant (and only) kernel: HIP events around replays of a graph of
     # back-to-back launches on the replay stream.
@@ -950,7 +957,8 @@ def main():
             "pool_blocks": a.pool_blocks,
             "max_ctx": a.max_ctx,
             "rotating_sets": nsets,
-            "step_launch": f"captured graphs of {nsets} back-to-back steps (one per set), as the decode replays them",
+            "step_launch": f"captured graphs of {GRAPH_STEPS} back-to-back steps cycling the {nsets} sets, as the "
+                           "decode replays one attention launch per layer in its graph of a token step",
             "rows": "longest-first, flagged SKV_ATTN_ROWS_LONGEST_FIRST (the graph decode's batch layout)",
             "chunk_tokens": a.chunk or native.default_chunk_tokens(a.batch, a.heads, a.head_dim, a.max_ctx, dtype),
             "library": native.version(),
