@@ -133,6 +133,26 @@ def test_gather_ragged_lengths_and_invalid_ids(cuda, bs, tmax):
     assert np.array_equal(vo.cpu().float().numpy(), want_v)
 
 
+@pytest.mark.parametrize("dtype,d,bs", [(torch.bfloat16, 128, 16), (torch.float16, 64, 64), (torch.float32, 32, 8),
+                                         (torch.bfloat16, 16, 32), (torch.float16, 16, 16), (torch.bfloat16, 80, 16)])
+def test_gather_row_widths_and_block_sizes(cuda, dtype, d, bs):
+    """Row widths of 1-16 16-byte vectors and block sizes 8-64: the wave path (8 lanes per 128-byte row,
+    a block id per load instruction) where the block holds one instruction's rows, the per-thread path
+    otherwise (16-wide bf16 rows in 16-key blocks; 80-wide rows). Output lengths that are not a multiple
+    of the wave's 32-row groups, lengths past the output, ids outside the pool: against the oracle."""
+    gen = torch.Generator().manual_seed(d * 10 + bs)
+    nb, h, maxblk, tmax = 48, 3, 5, 5 * bs - 3
+    kp, vp = make_pool(gen, nb, bs, h, d, dtype, cuda)
+    tables = make_tables(gen, 5, nb, maxblk)
+    tables[3, 2] = nb
+    lens = [tmax, 1, 0, 3 * bs + 1, tmax + 7]
+    ko, vo = native.gather(kp, vp, tables.to(cuda), torch.tensor(lens, dtype=torch.int32, device=cuda), tmax)
+    want_k = O.gather(kp.cpu().float().numpy(), tables.numpy(), lens, tmax)
+    want_v = O.gather(vp.cpu().float().numpy(), tables.numpy(), lens, tmax)
+    assert np.array_equal(ko.cpu().float().numpy(), want_k)
+    assert np.array_equal(vo.cpu().float().numpy(), want_v)
+
+
 def test_append_then_gather_round_trip(cuda):
     gen = torch.Generator().manual_seed(4)
     nb, bs, h, d, n = 128, 16, 8, 64, 300
