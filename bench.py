@@ -82,7 +82,7 @@ def parse():
     ap.add_argument("--decode-tokens", type=int, default=448)
     ap.add_argument("--decode-layers", type=int, default=32)
     ap.add_argument("--no-serving", action="store_true", help="skip the large-v3 256-request serving burst")
-    ap.add_argument("--mode", choices=["attention", "copy", "decode", "serving", "tts", "config1", "prefill",
+    ap.add_argument("--mode", choices=["attention", "copy", "decode", "decode-eager", "serving", "tts", "config1", "prefill",
                                        "copies"],
                     default="attention",
                     help="copy: plain device copy of --copy-mib MiB, a known-traffic kernel for counter scaling; "
@@ -522,8 +522,9 @@ def large_v3_argmax(torch, native, dev, a):
             "achieved_GBps": round(byts / (us * 1e-6) / 1e9, 1), "frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def large_v3_decode(torch, dev, a):
-    """Greedy decode of decode_batch requests x decode_tokens tokens through the scheduler's graphs."""
+def large_v3_decode(torch, dev, a, graph=True):
+    """Greedy decode of decode_batch requests x decode_tokens tokens through the scheduler: its captured
+    graphs (graph_decode=True), or its eager decode (the reference scheduler's default)."""
     from speech_serving import (BlockManager, DualCacheManager, EncoderBlockManager, MemoryGuard,
                                 PhaseAwareSpeechScheduler, WhisperClassSpeechEncoderDecoderModel)
     from speech_serving.phase_aware_scheduler import WHISPER_DEFAULT_PREFIX_TOKENS
@@ -536,8 +537,9 @@ def large_v3_decode(torch, dev, a):
     dec = BlockManager(L, h, 64, bs, num_blocks=b * per_req + 8, dtype=dt, device=str(dev))
     enc = EncoderBlockManager(1, h, 64, bs, num_blocks=8, dtype=dt, device=str(dev))
     sched = PhaseAwareSpeechScheduler(model, DualCacheManager(enc, dec), MemoryGuard(high_water_mark_pct=101.0),
-                                      max_batch_size=b, device=str(dev), eos_token_id=-1, graph_decode=True,
-                                      graph_readback_k=4, graph_direct_encoder_kv=True, graph_max_enc_len=t_enc)
+                                      max_batch_size=b, device=str(dev), eos_token_id=-1, graph_decode=graph,
+                                      **(dict(graph_readback_k=4, graph_direct_encoder_kv=True, graph_max_enc_len=t_enc)
+                                         if graph else {}))
     g = torch.Generator(device=dev).manual_seed(a.seed + 7)
     with torch.no_grad():
         for _ in range(b):
@@ -555,7 +557,8 @@ def large_v3_decode(torch, dev, a):
         "workload": f"Whisper-large-v3-shaped greedy decode: {L} layers, d_model {dm}, {h} heads x 64, vocab "
                     f"{vocab}, bf16 N(0,0.02) weights, {b} requests x {n} tokens from the 4-token prompt, "
                     f"{t_enc} N(0,1) encoder positions projected by cross_attn_k/v, block size {bs}, "
-                    f"graph decode (batch bucket {b}, readback every 4 steps)",
+                    + (f"graph decode (batch bucket {b}, readback every 4 steps)" if graph else
+                       "eager decode (decode_step with a PagedKVCache each step, the reference's default mode)"),
         "decode_tokens_per_s": round(decode_tokens / sched.decode_time_s, 1),
         "ms_per_decode_step": round(sched.decode_time_s / max(sched.decode_steps, 1) * 1e3, 3),
         "decode_steps": sched.decode_steps,
@@ -565,7 +568,7 @@ def large_v3_decode(torch, dev, a):
     }
     del sched, dec, enc
     torch.cuda.empty_cache()
-    if not a.no_cpu_baseline:
+    if graph and not a.no_cpu_baseline:
         res["cpu_baseline"] = decode_cpu_baseline(model, a.seed + 7, b, WHISPER_DEFAULT_PREFIX_TOKENS, 15.0)
     del model
     return res
@@ -829,6 +832,10 @@ def main():
         native.lib()
         print(json.dumps({"large_v3_decode": large_v3_decode(torch, dev, a)}))
         return
+    if a.mode == "decode-eager":  # the same decode in the scheduler's eager mode
+        native.lib()
+        print(json.dumps({"large_v3_decode_eager": large_v3_decode(torch, dev, a, graph=False)}))
+        return
     if a.mode == "serving":  # the large-v3 serving burst alone
         native.lib()
         print(json.dumps({"large_v3_serving": large_v3_serving(torch, dev, a)}))
@@ -1005,6 +1012,7 @@ def main():
     if not a.no_large_v3:
         if not a.no_decode:
             result["large_v3_decode"] = large_v3_decode(torch, dev, a)
+            result["large_v3_decode_eager"] = large_v3_decode(torch, dev, a, graph=False)
         if not a.no_serving:
             result["large_v3_serving"] = large_v3_serving(torch, dev, a)
     # Free the legs' host and device memory before the line is printed, so the process ends promptly.

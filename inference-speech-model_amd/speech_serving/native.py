@@ -13,6 +13,7 @@ Functions:
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 from typing import Dict, Optional, Sequence, Tuple
@@ -142,11 +143,18 @@ def _code(dtype: torch.dtype) -> int:
 
 
 def _gpu(t: torch.Tensor, name: str) -> None:
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise RuntimeError(f"{name} must be a GPU tensor (got device {t.device}); the HIP kernels have no CPU path")
 
 
+# The current stream's raw handle without building a torch.cuda.Stream object (the per-call host
+# cost of every entry point below).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(torch.cuda.current_device() if device.index is None else device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
@@ -171,7 +179,7 @@ _workspaces: Dict[int, torch.Tensor] = {}
 
 
 def _dev_index(device) -> int:
-    idx = torch.device(device).index
+    idx = (device if isinstance(device, torch.device) else torch.device(device)).index
     return torch.cuda.current_device() if idx is None else idx
 
 
@@ -203,20 +211,38 @@ def _scratch(need: int, device):
     return ws.data_ptr(), ws.numel()
 
 
+# The sizing queries are pure functions of their arguments: memoised, so a decode step's calls
+# cost a dictionary lookup rather than a foreign call each.
+@functools.lru_cache(maxsize=4096)
+def _workspace_bytes(rows: int, heads: int, head_dim: int, max_len: int, chunk_tokens: int, code: int) -> int:
+    return int(lib().skv_attention_workspace_bytes(rows, heads, head_dim, max_len, chunk_tokens, code))
+
+
+@functools.lru_cache(maxsize=4096)
+def _default_chunk(rows: int, heads: int, head_dim: int, max_len: int, code: int) -> int:
+    return int(lib().skv_default_chunk_tokens(rows, heads, head_dim, max_len, code))
+
+
+@functools.lru_cache(maxsize=4096)
+def _paged_chunk(rows: int, heads: int, kv_heads: int, head_dim: int, max_ctx: int, code: int, block_size: int,
+                 num_blocks: int) -> int:
+    return int(lib().skv_paged_chunk_tokens(rows, heads, kv_heads, head_dim, max_ctx, code, block_size, num_blocks))
+
+
 def attention_workspace_bytes(rows: int, heads: int, head_dim: int, max_len: int, dtype: torch.dtype,
                               chunk_tokens: int = 0) -> int:
-    return int(lib().skv_attention_workspace_bytes(rows, heads, head_dim, max_len, chunk_tokens, _code(dtype)))
+    return _workspace_bytes(int(rows), int(heads), int(head_dim), int(max_len), int(chunk_tokens), _code(dtype))
 
 
 def default_chunk_tokens(rows: int, heads: int, head_dim: int, max_len: int, dtype: torch.dtype) -> int:
-    return int(lib().skv_default_chunk_tokens(rows, heads, head_dim, max_len, _code(dtype)))
+    return _default_chunk(int(rows), int(heads), int(head_dim), int(max_len), _code(dtype))
 
 
 def paged_chunk_tokens(rows: int, heads: int, kv_heads: int, head_dim: int, max_ctx: int, dtype: torch.dtype,
                        block_size: int, num_blocks: int) -> int:
     """The chunk skv_paged_attention takes by default for pools of num_blocks x block_size tokens."""
-    return int(lib().skv_paged_chunk_tokens(rows, heads, kv_heads, head_dim, max_ctx, _code(dtype), block_size,
-                                            num_blocks))
+    return _paged_chunk(int(rows), int(heads), int(kv_heads), int(head_dim), int(max_ctx), _code(dtype),
+                        int(block_size), int(num_blocks))
 
 
 # ---------------------------------------------------------------------------
@@ -572,10 +598,12 @@ def add_layernorm(x: torch.Tensor, y: Optional[torch.Tensor], weight: torch.Tens
     """
     _gpu(x, "x")
     h = x.shape[-1]
-    if not add_layernorm_supported(x, weight):
+    epl = 16 // x.element_size()
+    rows = x.numel() // h if h else 0
+    x2 = x.reshape(rows, h) if rows else x
+    if x.dtype not in _DTYPE_CODE or weight.dtype != x.dtype or h % epl or h > 512 * epl or x.stride(-1) != 1 or \
+            (rows and (x2.stride(0) % epl or x2.data_ptr() % 16)):
         raise RuntimeError("add_layernorm: unsupported dtype/hidden size/layout")
-    rows = x.numel() // h
-    x2 = x.reshape(rows, h)
     y2 = None
     if y is not None:
         _gpu(y, "y")
