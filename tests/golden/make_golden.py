@@ -6,8 +6,9 @@ Run in the development container, where the reference repository is mounted:
 
 --lowp writes tests/golden/whisper_lowp_golden.npz: the reference's own reduced-precision greedy
 decode (its model in float16 and in bfloat16 on the CPU, decode_step with a DynamicCache, torch.argmax
-per step) for two shapes, the golden tiny shape and a Whisper-tiny-like decoder (4 layers, d_model 384,
-4 heads x 64, vocab 51865, 1500 encoder positions, the Whisper prompt), two requests each: per step the
+per step) for four shapes, the golden tiny shape, a Whisper-tiny-like decoder (4 layers, d_model 384,
+4 heads x 64), a base-shaped (6 layers, 512, 8 x 64) and a small-shaped one (12 layers, 768, 12 x 64), the
+last three with vocab 51865, 1500 encoder positions and the Whisper prompt, two requests each: per step the
 token and the top-16 logits (index, value); for the tiny shape every logit. Weights and encoder K/V are
 regenerated from seeds by name (oracle/rounding.seeded_state / seeded_cross_kv); the file records their
 checksums so a run that regenerates them can check it has the same inputs.
@@ -96,6 +97,14 @@ LOWP_SHAPES = {
     "c1": dict(layers=4, heads=4, hidden=384, head_dim=64, vocab=51865, t_enc=1500,
                prompt=[50258, 50259, 50359, 50363], steps=32, std=0.02, kv_std=0.4, seed=2201,
                kv_seeds=[2202, 2203]),
+    # the base-shaped (6 layers, 512, 8 x 64) and small-shaped (12 layers, 768, 12 x 64) decoders of the
+    # serving scenarios
+    "c3": dict(layers=6, heads=8, hidden=512, head_dim=64, vocab=51865, t_enc=1500,
+               prompt=[50258, 50259, 50359, 50363], steps=24, std=0.02, kv_std=0.4, seed=2301,
+               kv_seeds=[2302, 2303]),
+    "c4": dict(layers=12, heads=12, hidden=768, head_dim=64, vocab=51865, t_enc=1500,
+               prompt=[50258, 50259, 50359, 50363], steps=24, std=0.03, kv_std=0.4, seed=2401,
+               kv_seeds=[2402, 2403]),
 }
 LOWP_DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16}
 TOPK = 16

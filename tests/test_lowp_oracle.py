@@ -9,9 +9,11 @@
   reference's token except at near-ties;
 - the rounding emulation that rounds where the reference rounds reproduces the reference's logits
   (bit for bit on every tiny-shape fixture: the top-16 logits of every step, and all 100 logits of every step
-  of at least two of them; within a few dtype steps at the Whisper-tiny-like shape), while a
-  misplaced set of rounding sites (the paged path's, which keeps attention scores and probabilities in
-  fp32) does not: the site list is pinned by the reference's arithmetic.
+  of at least two of them), while a misplaced set of rounding sites (the paged path's, which keeps attention
+  scores and probabilities in fp32) does not: the site list is pinned by the reference's arithmetic. At the
+  larger shapes (Whisper-tiny-like, base- and small-shaped) the reference's fp32 accumulation order moves
+  logits by a few dtype steps whichever sites are rounded, so there the emulation is held to the reference's
+  rounding model (its logits within 5 sigma, its tokens the reference's except at near-ties).
 """
 import json
 import os
@@ -94,15 +96,18 @@ def test_rounding_emulation_reproduces_the_reference(lowp):
             # logits lie within the reference's own rounding model, and its tokens are the reference's except
             # at near-ties.
             LC.compare(ref, em["reference"].numpy(), f"reference-site emulation vs {key}")
-            assert (steps["reference"] == 0).mean() >= (steps["paged"] == 0).mean(), key
-            if shape == "tiny" and (steps["reference"] == 0).all():
-                exact_cases += 1
-                assert (steps["paged"] > 0).any(), key
-                full = z[f"{key}.logits"].astype(np.float64)
-                full_exact += int(np.array_equal(em["reference"].numpy(), full))
             print(f"{key}: logits equal to the reference's bit for bit: {(steps['reference'] == 0).mean():.3f} "
                   f"(misplaced sites {(steps['paged'] == 0).mean():.3f}); largest gap {steps['reference'].max():.0f} "
                   f"dtype steps (misplaced sites {steps['paged'].max():.0f})")
+            if shape == "tiny":
+                # sums short enough that the reference's fp32 accumulation order does not show: the site list
+                # decides, and only the reference's sites reproduce its logits
+                assert (steps["reference"] == 0).mean() > (steps["paged"] == 0).mean(), key
+                if (steps["reference"] == 0).all():
+                    exact_cases += 1
+                    assert (steps["paged"] > 0).any(), key
+                    full = z[f"{key}.logits"].astype(np.float64)
+                    full_exact += int(np.array_equal(em["reference"].numpy(), full))
     # every tiny-shape fixture: the top-16 logits of every step bit for bit (all 100 logits of every step in at
     # least two of them)
     assert exact_cases == 4 and full_exact >= 2

@@ -1,8 +1,9 @@
 """fp16 / bf16 greedy decoding on the GPU against the reference's own reduced-precision decodes
 (tests/golden/whisper_lowp_golden.npz: the reference's models.py cast to float16 / bfloat16 and decoded
-greedily on the CPU), for the golden tiny shape and a Whisper-tiny-like decoder (4 layers, d_model 384,
-4 heads x 64, vocab 51865, 1500 encoder positions, the Whisper prompt). The GPU model takes the same
-seeded weights and encoder K/V.
+greedily on the CPU), for the golden tiny shape, a Whisper-tiny-like decoder (4 layers, d_model 384,
+4 heads x 64) and the base- and small-shaped decoders of the serving scenarios (6 layers, 512, 8 x 64;
+12 layers, 768, 12 x 64), all with vocab 51865, 1500 encoder positions and the Whisper prompt. The GPU
+model takes the same seeded weights and encoder K/V.
 
 - Teacher-forced along the reference's tokens (both requests as one batch through decode_step with a
   PagedKVCache, the scheduler's eager path): at every step the top-1 logit and the top-2 margin lie within
@@ -13,6 +14,8 @@ seeded weights and encoder K/V.
 - Free-running through the scheduler (eager and graph decode, both requests batched): the GPU's tokens are
   the reference's up to the first near-tie of the reference's decode (the whole stream when it has none).
 """
+import functools
+
 import numpy as np
 import pytest
 import torch
@@ -39,7 +42,11 @@ def gpu_model(c, state, cuda, dtype):
     return m.to(cuda, dtype).eval()
 
 
-def setup(shape, dname, cuda):
+@functools.lru_cache(maxsize=None)
+def setup(shape, dname):
+    """The case's config, dtype, seeded weights and encoder K/V (checked against the fixture), float64
+    decoder, and per request the reference's error model against the reference (both site sets) and
+    against float64 (the paged sites): built once per case, shared by the tests below."""
     c = CFG["shapes"][shape]
     dt = LC.DTYPES[dname]
     names = {k: tuple(v.shape) for k, v in WhisperClassSpeechEncoderDecoderModel(
@@ -47,7 +54,11 @@ def setup(shape, dname, cuda):
     state = LC.model_state(c, names, dt)
     crosses = [LC.cross_kv(c, r, dt) for r in range(len(c["kv_seeds"]))]
     LC.check_inputs(Z, shape, dname, state, crosses)
-    return c, dt, state, crosses
+    dec64 = Decoder64(state, c["heads"], c["head_dim"])
+    keys = [f"{shape}.{dname}.r{r}" for r in range(len(crosses))]
+    refs = [LC.Reference(Z, c, k, dec64, crosses[r], dt, ("reference", "paged")) for r, k in enumerate(keys)]
+    exact = [LC.Reference(Z, c, k, dec64, crosses[r], dt, ("paged",), float64=True) for r, k in enumerate(keys)]
+    return c, dt, state, crosses, keys, refs, exact
 
 
 def teacher_forced(m, c, dt, crosses, paths, cuda):
@@ -76,12 +87,8 @@ def teacher_forced(m, c, dt, crosses, paths, cuda):
 
 @pytest.mark.parametrize("shape,dname", CASES)
 def test_teacher_forced_logits_and_tokens_against_the_reference(cuda, shape, dname):
-    c, dt, state, crosses = setup(shape, dname, cuda)
+    c, dt, state, crosses, keys, refs, exact = setup(shape, dname)
     m = gpu_model(c, state, cuda, dt)
-    dec64 = Decoder64(state, c["heads"], c["head_dim"])
-    keys = [f"{shape}.{dname}.r{r}" for r in range(len(crosses))]
-    refs = [LC.Reference(Z, c, k, dec64, crosses[r], dt, ("reference", "paged")) for r, k in enumerate(keys)]
-    exact = [LC.Reference(Z, c, k, dec64, crosses[r], dt, ("paged",), float64=True) for r, k in enumerate(keys)]
     got = teacher_forced(m, c, dt, crosses, [ref.tokens for ref in refs], cuda)
     for r, (ref, ex) in enumerate(zip(refs, exact)):
         a = LC.compare(ref, got[r], f"GPU vs the reference's {keys[r]}")
@@ -94,9 +101,8 @@ def test_teacher_forced_logits_and_tokens_against_the_reference(cuda, shape, dna
 @pytest.mark.parametrize("mode", ["eager", "graph"])
 @pytest.mark.parametrize("shape,dname", CASES)
 def test_free_running_tokens_follow_the_reference(cuda, shape, dname, mode):
-    c, dt, state, crosses = setup(shape, dname, cuda)
+    c, dt, state, crosses, keys, refs, _ = setup(shape, dname)
     m = gpu_model(c, state, cuda, dt)
-    dec64 = Decoder64(state, c["heads"], c["head_dim"])
     steps = len(Z[f"{shape}.{dname}.r0.tokens"])
     pool = len(crosses) * (-(-(len(c["prompt"]) + steps) // BS)) + 8
     dec = BlockManager(c["layers"], c["heads"], c["head_dim"], BS, num_blocks=pool, dtype=dt, device=str(cuda))
@@ -111,8 +117,7 @@ def test_free_running_tokens_follow_the_reference(cuda, shape, dname, mode):
     done = sorted(s.run_until_done(), key=lambda q: q.id)
     assert dec.allocated_block_count == 0
     for r, q in enumerate(done):
-        key = f"{shape}.{dname}.r{r}"
-        ref = LC.Reference(Z, c, key, dec64, crosses[r], dt, ("reference", "paged"))
+        key, ref = keys[r], refs[r]
         ties = np.nonzero(ref.near_tie)[0]
         limit = int(ties[0]) if ties.size else steps  # the steps before the reference's first near-tie
         same = 0
