@@ -21,10 +21,16 @@ module gives that difference a derived size, with no constant fitted to measurem
 - seeded_state / seeded_cross_kv regenerate the fixtures' weights and encoder K/V from seeds, by
   parameter name, so the reference run and the GPU run use identical inputs.
 
+- MultiCodebook64 does the same for the streaming multi-codebook TTS model (models.py:23-77, 211-295):
+  the K codebook embeddings summed left to right (each partial sum a site), the same layers without
+  cross-attention, the final norm and K heads, with the K heads' logits laid out as one row.
+
 Parity pins: Decoder64's float64 logits equal oracle/decoder.py (itself pinned by the reference's
 golden vectors) on the golden model; the reference's own fp16/bf16 logits (tests/golden/
 whisper_lowp_golden.npz) lie within 5 sigma of Decoder64's float64 logits at every checked step
-(tests/test_lowp_oracle.py).
+(tests/test_lowp_oracle.py). MultiCodebook64 equals oracle/tts.py (pinned by the reference's TTS golden
+vectors) on the golden TTS model, and the reference's own fp16/bf16 TTS logits (tests/golden/
+tts_lowp_golden.npz) lie within 5 sigma of it (tests/test_tts_lowp_oracle.py).
 """
 from __future__ import annotations
 
@@ -95,59 +101,109 @@ def ulp(y: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return torch.exp2(e - (p - 1))
 
 
+def _ln(x, w, b):
+    return torch.nn.functional.layer_norm(x, (x.shape[-1],), w, b, 1e-5)
+
+
+def _layers(x: torch.Tensor, n_layers: int, h: int, d: int, layer_w, cross, site) -> torch.Tensor:
+    """The decoder layers of models.py:110-208 over one request's sequence x [S, hidden] (causal
+    self-attention, cross-attention over cross[i] where given, GELU MLP): layer_w(i, name) gives a
+    weight, site(i, name, y) takes each rounding site's value and returns what the layer goes on with
+    (the value itself, or the value rounded)."""
+    s = x.shape[0]
+    scale = 1.0 / math.sqrt(d)
+    causal = torch.triu(torch.full((s, s), float("-inf"), dtype=torch.float64), diagonal=1)
+    for i in range(n_layers):
+        L = lambda n, i=i: layer_w(i, n)  # noqa: E731
+        r = lambda n, y, i=i: site(i, n, y)  # noqa: E731
+        h1 = r("norm1", _ln(x, L("norm1.weight"), L("norm1.bias")))
+        q = r("q", h1 @ L("self_attn_q.weight").T).view(s, h, d).transpose(0, 1)
+        k = r("k", h1 @ L("self_attn_k.weight").T).view(s, h, d).transpose(0, 1)
+        v = r("v", h1 @ L("self_attn_v.weight").T).view(s, h, d).transpose(0, 1)
+        w = r("scores", q @ k.transpose(1, 2)) * scale + causal
+        pr = r("probs", torch.softmax(w, dim=-1))
+        o = r("attn", pr @ v).transpose(0, 1).reshape(s, h * d)
+        x = r("res1", x + r("attn_out", o @ L("self_attn_out.weight").T))
+        used = cross is not None and i < len(cross)
+        if used:
+            ck, cv = cross[i]
+            h2 = r("norm2", _ln(x, L("norm2.weight"), L("norm2.bias")))
+            cq = r("cq", h2 @ L("cross_attn_q.weight").T).view(s, h, d).transpose(0, 1)
+            cw = r("cscores", cq @ ck.transpose(1, 2)) * scale
+            cp = r("cprobs", torch.softmax(cw, dim=-1))
+            co = r("cattn", cp @ cv).transpose(0, 1).reshape(s, h * d)
+            x = r("res2", x + r("cattn_out", co @ L("cross_attn_out.weight").T))
+        n = "norm3" if used else "norm2"
+        hm = r(n, _ln(x, L(f"{n}.weight"), L(f"{n}.bias")))
+        f1 = r("fc1", hm @ L("mlp.0.weight").T + L("mlp.0.bias"))
+        gl = r("gelu", torch.nn.functional.gelu(f1))
+        x = r("res3", x + r("fc2", gl @ L("mlp.2.weight").T + L("mlp.2.bias")))
+    return x
+
+
 class Decoder64:
     """Float64 restatement of the reference decoder (models.py:110-208, 369-423) over one request's whole
     token sequence, causal, with per-layer cross-attention over given encoder K/V."""
 
+    layer_prefix = "decoder_layers"
+
     def __init__(self, state: Dict[str, torch.Tensor], num_heads: int, head_dim: int):
         self.p = {k: v.detach().to(torch.float64) for k, v in state.items()}
         self.h, self.d = num_heads, head_dim
-        self.layers = len({k.split(".")[1] for k in state if k.startswith("decoder_layers.")})
+        self.layers = len({k.split(".")[1] for k in state if k.startswith(self.layer_prefix + ".")})
 
-    @staticmethod
-    def _ln(x, w, b):
-        return torch.nn.functional.layer_norm(x, (x.shape[-1],), w, b, 1e-5)
+    _ln = staticmethod(_ln)
 
-    def forward(self, ids: Sequence[int], cross: Optional[Sequence[Tuple[torch.Tensor, torch.Tensor]]],
+    # The model's two ends: the input rows, and the logits as a [S, V] matrix (the multi-codebook model
+    # flattens its K heads into [S, K * V]). W(name) gives a weight, site(name, y) takes a rounding site,
+    # start(x) takes the first gathered rows (a graph leaf when sites are recorded).
+    def embed(self, ids, W, site, start) -> torch.Tensor:
+        return start(W("decoder_embed.weight")[torch.as_tensor(list(ids))])
+
+    def head(self, x, W, site) -> torch.Tensor:
+        hf = site("final_norm", _ln(x, W("decoder_norm.weight"), W("decoder_norm.bias")))
+        return site("logits", hf @ W("lm_head.weight").T)
+
+    def run(self, ids, cross, site, W, cast=lambda t: t, leaf: bool = False) -> torch.Tensor:
+        """The pass with site(name, y) at every rounding site ("<layer>.<site>" inside the layers), weights
+        from W, the input rows and encoder K/V through cast; leaf: the input rows become a graph leaf."""
+        start = (lambda t: cast(t).clone().requires_grad_(True)) if leaf else cast
+        x = cast(self.embed(ids, W, site, start))
+        cr = None if cross is None else [tuple(cast(t.detach().to(torch.float64)[0]) for t in kv) for kv in cross]
+        x = _layers(x, self.layers, self.h, self.d, lambda i, n: W(f"{self.layer_prefix}.{i}.{n}"), cr,
+                    lambda i, n, y: site(f"{i}.{n}", y))
+        return self.head(x, W, site)
+
+    def forward(self, ids: Sequence, cross: Optional[Sequence[Tuple[torch.Tensor, torch.Tensor]]],
                 sites: Optional[Dict[str, torch.Tensor]] = None) -> torch.Tensor:
         """logits [S, V] of the token sequence ids (row t: the step that sees tokens 0..t). With `sites`,
         every rounding site's float64 value is recorded under "<layer>.<site>" (kept in the graph)."""
-        P = self.p
-        h, d = self.h, self.d
-        rec = (lambda n, y: sites.__setitem__(n, y) or y) if sites is not None else (lambda n, y: y)
-        x = P["decoder_embed.weight"][torch.as_tensor(list(ids))]
-        if sites is not None:
-            x = x.clone().requires_grad_(True)
-        s = x.shape[0]
-        scale = 1.0 / math.sqrt(d)
-        causal = torch.triu(torch.full((s, s), float("-inf"), dtype=torch.float64), diagonal=1)
-        for i in range(self.layers):
-            L = lambda n: P[f"decoder_layers.{i}.{n}"]  # noqa: E731
-            r = lambda n, y, i=i: rec(f"{i}.{n}", y)  # noqa: E731
-            h1 = r("norm1", self._ln(x, L("norm1.weight"), L("norm1.bias")))
-            q = r("q", h1 @ L("self_attn_q.weight").T).view(s, h, d).transpose(0, 1)
-            k = r("k", h1 @ L("self_attn_k.weight").T).view(s, h, d).transpose(0, 1)
-            v = r("v", h1 @ L("self_attn_v.weight").T).view(s, h, d).transpose(0, 1)
-            w = r("scores", q @ k.transpose(1, 2)) * scale + causal
-            pr = r("probs", torch.softmax(w, dim=-1))
-            o = r("attn", pr @ v).transpose(0, 1).reshape(s, h * d)
-            x = r("res1", x + r("attn_out", o @ L("self_attn_out.weight").T))
-            used = cross is not None and i < len(cross)
-            if used:
-                ck, cv = (t.detach().to(torch.float64)[0] for t in cross[i])
-                h2 = r("norm2", self._ln(x, L("norm2.weight"), L("norm2.bias")))
-                cq = r("cq", h2 @ L("cross_attn_q.weight").T).view(s, h, d).transpose(0, 1)
-                cw = r("cscores", cq @ ck.transpose(1, 2)) * scale
-                cp = r("cprobs", torch.softmax(cw, dim=-1))
-                co = r("cattn", cp @ cv).transpose(0, 1).reshape(s, h * d)
-                x = r("res2", x + r("cattn_out", co @ L("cross_attn_out.weight").T))
-            n = "norm3" if used else "norm2"
-            hm = r("norm3" if used else "norm2", self._ln(x, L(f"{n}.weight"), L(f"{n}.bias")))
-            f1 = r("fc1", hm @ L("mlp.0.weight").T + L("mlp.0.bias"))
-            gl = r("gelu", torch.nn.functional.gelu(f1))
-            x = r("res3", x + r("fc2", gl @ L("mlp.2.weight").T + L("mlp.2.bias")))
-        hf = rec("final_norm", self._ln(x, P["decoder_norm.weight"], P["decoder_norm.bias"]))
-        return rec("logits", hf @ P["lm_head.weight"].T)
+        if sites is None:
+            return self.run(ids, cross, lambda n, y: y, self.p.__getitem__)
+        return self.run(ids, cross, lambda n, y: sites.__setitem__(n, y) or y, self.p.__getitem__, leaf=True)
+
+
+class MultiCodebook64(Decoder64):
+    """Float64 restatement of the reference's streaming multi-codebook TTS model (models.py:23-77,
+    211-295): the frame's input is the sum of its K codebook embeddings, added left to right (each
+    partial sum a rounding site, "emb<k>"), the decoder layers without cross-attention, the final norm
+    ("norm") and K linear heads. A sequence is a list of frames (K codes each); the logits of the K
+    heads are laid out as one row [K * V] per position (head k's token j at k * V + j)."""
+
+    layer_prefix = "layers"
+
+    def embed(self, frames, W, site, start) -> torch.Tensor:
+        codes = torch.as_tensor([list(f) for f in frames])
+        k_n = codes.shape[1]
+        x = start(W("embeddings.embeddings.0.weight")[codes[:, 0]])
+        for k in range(1, k_n):
+            x = site(f"emb{k}", x + W(f"embeddings.embeddings.{k}.weight")[codes[:, k]])
+        return x
+
+    def head(self, x, W, site) -> torch.Tensor:
+        hf = site("final_norm", _ln(x, W("norm.weight"), W("norm.bias")))
+        k_n = len([n for n in self.p if n.startswith("heads.heads.")])
+        return site("logits", torch.cat([hf @ W(f"heads.heads.{k}.weight").T for k in range(k_n)], dim=-1))
 
 
 def _site_kind(name: str) -> str:
@@ -182,40 +238,10 @@ def rounding_sigma(model: Decoder64, ids: Sequence[int], cross, dtype: torch.dty
     return torch.tensor(sig, dtype=torch.float64), logits.detach()
 
 
-def round_through(model: Decoder64, ids: Sequence[int], cross, dtype: torch.dtype, placement: str) -> torch.Tensor:
+def round_through(model: Decoder64, ids: Sequence, cross, dtype: torch.dtype, placement: str) -> torch.Tensor:
     """The float64 pass with every site of `placement` rounded to dtype (round to nearest even) where it
-    is produced: an emulation of that implementation's arithmetic up to its fp32 accumulation order."""
+    is produced, from weights, input rows and encoder K/V in dtype: an emulation of that implementation's
+    arithmetic up to its fp32 accumulation order."""
     skip = PAGED_SKIPS if placement == "paged" else frozenset()
-    P = model.p
-    rnd = lambda n, y: y if n in skip else y.to(dtype).to(torch.float64)  # noqa: E731
-    h, d = model.h, model.d
-    x = P["decoder_embed.weight"][torch.as_tensor(list(ids))].to(dtype).to(torch.float64)
-    s = x.shape[0]
-    scale = 1.0 / math.sqrt(d)
-    causal = torch.triu(torch.full((s, s), float("-inf"), dtype=torch.float64), diagonal=1)
-    W = lambda n: P[n].to(dtype).to(torch.float64)  # noqa: E731
-    for i in range(model.layers):
-        L = lambda n, i=i: W(f"decoder_layers.{i}.{n}")  # noqa: E731
-        h1 = rnd("norm1", Decoder64._ln(x, L("norm1.weight"), L("norm1.bias")))
-        q = rnd("q", h1 @ L("self_attn_q.weight").T).view(s, h, d).transpose(0, 1)
-        k = rnd("k", h1 @ L("self_attn_k.weight").T).view(s, h, d).transpose(0, 1)
-        v = rnd("v", h1 @ L("self_attn_v.weight").T).view(s, h, d).transpose(0, 1)
-        w = rnd("scores", q @ k.transpose(1, 2)) * scale + causal
-        pr = rnd("probs", torch.softmax(w, dim=-1))
-        o = rnd("attn", pr @ v).transpose(0, 1).reshape(s, h * d)
-        x = rnd("res1", x + rnd("attn_out", o @ L("self_attn_out.weight").T))
-        used = cross is not None and i < len(cross)
-        if used:
-            ck, cv = (t.detach().to(dtype).to(torch.float64)[0] for t in cross[i])
-            h2 = rnd("norm2", Decoder64._ln(x, L("norm2.weight"), L("norm2.bias")))
-            cq = rnd("cq", h2 @ L("cross_attn_q.weight").T).view(s, h, d).transpose(0, 1)
-            cw = rnd("cscores", cq @ ck.transpose(1, 2)) * scale
-            cp = rnd("cprobs", torch.softmax(cw, dim=-1))
-            co = rnd("cattn", cp @ cv).transpose(0, 1).reshape(s, h * d)
-            x = rnd("res2", x + rnd("cattn_out", co @ L("cross_attn_out.weight").T))
-        n = "norm3" if used else "norm2"
-        hm = rnd(n, Decoder64._ln(x, L(f"{n}.weight"), L(f"{n}.bias")))
-        gl = rnd("gelu", torch.nn.functional.gelu(rnd("fc1", hm @ L("mlp.0.weight").T + L("mlp.0.bias"))))
-        x = rnd("res3", x + rnd("fc2", gl @ L("mlp.2.weight").T + L("mlp.2.bias")))
-    hf = rnd("final_norm", Decoder64._ln(x, W("decoder_norm.weight"), W("decoder_norm.bias")))
-    return rnd("logits", hf @ W("lm_head.weight").T)
+    rt = lambda y: y.to(dtype).to(torch.float64)  # noqa: E731
+    return model.run(ids, cross, lambda n, y: y if _site_kind(n) in skip else rt(y), lambda n: rt(model.p[n]), rt)

@@ -1,8 +1,18 @@
 """Write golden vectors of the reference's streaming multi-codebook TTS model and engine.
 
 Run in the development container, where the reference repository is mounted:
-    python tests/golden/make_tts_golden.py [/path/to/reference]
-It imports speech_serving.models.StreamingMultiCodebookTTSModel and
+    python tests/golden/make_tts_golden.py [/path/to/reference]          # float32 vectors
+    python tests/golden/make_tts_golden.py [/path/to/reference] --lowp   # fp16 / bf16 greedy frames
+
+--lowp writes tests/golden/tts_lowp_golden.npz: the reference's own reduced-precision greedy decode
+(its StreamingMultiCodebookTTSModel cast to float16 and to bfloat16 on the CPU, model(...) with a
+DynamicCache per frame, argmax per codebook) for two shapes, the float32 golden shape below and the
+reference model's default shape (4 layers, 4 heads x 64, 4 codebooks, vocab 1024), two requests each:
+per frame the K codes and each codebook's top-16 logits (for the small shape every logit). Weights and
+prompts are drawn from seeds by name (oracle/rounding.seeded_state, numpy PCG64), so a run that
+regenerates them checks the recorded checksums.
+
+The float32 mode imports speech_serving.models.StreamingMultiCodebookTTSModel and
 speech_serving.tts_engine.StreamingTTSEngine from the reference (CPU,
 float32), builds a small seeded model with the shapes of the reference's own
 TTS test (test_speech_engine.py:35-91), and saves to
@@ -115,5 +125,75 @@ def main(ref_root: str) -> None:
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(out)} arrays), seed {seed}, min margin {margin:.4g}")
 
 
+LOWP_OUT = os.path.join(HERE, "tts_lowp_golden.npz")
+LOWP_SHAPES = {
+    # layers, heads, hidden, codebooks, vocab, prompt frames, generated frames, weight std, seeds
+    "small": dict(num_layers=2, num_heads=4, hidden_dim=64, num_codebooks=4, vocab_size=128, prompt_len=8,
+                  frames=16, std=0.1, seed=3101, prompt_seeds=[3102, 3103]),
+    "default": dict(num_layers=4, num_heads=4, hidden_dim=256, num_codebooks=4, vocab_size=1024, prompt_len=8,
+                    frames=16, std=0.05, seed=3201, prompt_seeds=[3202, 3203]),
+}
+LOWP_DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16}
+TOPK = 16
+
+
+def lowp_prompt(cfg, seed):
+    """[P, K] int64 prompt frames, uniform codes from one numpy PCG64 stream."""
+    g = np.random.default_rng(seed)
+    return g.integers(0, cfg["vocab_size"], size=(cfg["prompt_len"], cfg["num_codebooks"]), dtype=np.int64)
+
+
+def write_lowp(ref_root: str) -> None:
+    sys.path.insert(0, ref_root)
+    sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))  # the repository root, for oracle/
+    from speech_serving.models import StreamingMultiCodebookTTSModel  # noqa: E402  (reference)
+
+    from oracle.rounding import checksums, seeded_state  # noqa: E402
+
+    out = {}
+    for shape, cfg in LOWP_SHAPES.items():
+        args = {k: cfg[k] for k in ("num_layers", "num_heads", "hidden_dim", "num_codebooks", "vocab_size")}
+        for dname, dtype in LOWP_DTYPES.items():
+            model = StreamingMultiCodebookTTSModel(**args)
+            state = seeded_state({k: tuple(v.shape) for k, v in model.state_dict().items()}, cfg["seed"], cfg["std"])
+            model.load_state_dict(state)
+            model = model.to(dtype).eval()
+            out[f"{shape}.{dname}.param_checksums"] = checksums({k: v.to(dtype) for k, v in state.items()}).numpy()
+            for r, pseed in enumerate(cfg["prompt_seeds"]):
+                key = f"{shape}.{dname}.r{r}"
+                prompt = lowp_prompt(cfg, pseed)
+                frames, tk_i, tk_v, full = [], [], [], []
+                with torch.no_grad():
+                    cur = model(input_codebooks=torch.from_numpy(prompt)[None], use_cache=True)
+                    for _ in range(cfg["frames"]):
+                        last = cur.logits[0, -1]  # [K, V]
+                        vals, idx = torch.topk(last.float(), TOPK, dim=-1)
+                        tk_i.append(idx.numpy())
+                        tk_v.append(vals.numpy())
+                        if shape == "small":
+                            full.append(last.float().numpy())
+                        nxt = torch.argmax(last, dim=-1)
+                        frames.append(nxt.numpy())
+                        cur = model(input_codebooks=nxt[None, None], past_key_values=cur.past_key_values,
+                                    use_cache=True)
+                out[f"{key}.prompt"] = prompt
+                out[f"{key}.frames"] = np.stack(frames).astype(np.int64)
+                out[f"{key}.topk_idx"] = np.stack(tk_i).astype(np.int64)
+                out[f"{key}.topk_val"] = np.stack(tk_v).astype(np.float32)
+                if full:
+                    out[f"{key}.logits"] = np.stack(full).astype(np.float32)
+                print(f"  {key}: frames {[f.tolist() for f in frames[:4]]} ... distinct codes "
+                      f"{len(set(np.stack(frames).reshape(-1).tolist()))}")
+    out["config_json"] = np.frombuffer(json.dumps(dict(shapes=LOWP_SHAPES, dtypes=list(LOWP_DTYPES),
+                                                       topk=TOPK)).encode(), dtype=np.uint8)
+    np.savez_compressed(LOWP_OUT, **out)
+    print(f"wrote {LOWP_OUT} ({os.path.getsize(LOWP_OUT)} bytes, {len(out)} arrays)")
+
+
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    root = args[0] if args else "/root/reference"
+    if "--lowp" in sys.argv[1:]:
+        write_lowp(root)
+    else:
+        main(root)
