@@ -400,6 +400,14 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
   float best = kNegInf;
   int bi = 4 * (int)threadIdx.x < nw ? head + EPW * 4 * (int)threadIdx.x : 0x7fffffff;
   float nmax = kNegInf;  // NaN-propagating maximum of the thread's elements: NaN flags a NaN
+  // Slot feedback inputs load while the row streams in: wave 0, which writes the feedback, reads
+  // the row's slot and then the slot's EOS id and finished flag once its first pass's loads are
+  // issued, so the end of the kernel waits for no dependent load. Empty asm statements with a
+  // memory clobber keep these loads behind the pass's loads.
+  const bool wave0 = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) == 0;
+  int slot = -1;
+  int64_t slot_eos = -1;
+  int slot_fin = 1;
   // Thread t's vectors: words 4 * (t + kArgmaxThreads * k) .. +3, k = 0, 1, ...
   constexpr int kPassWords = 4 * kArgmaxThreads * VECS;
   constexpr int kVecElts = 4 * EPW;
@@ -409,6 +417,13 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
     for (int k = 0; k < VECS; ++k)
       x[k] = __builtin_amdgcn_raw_buffer_load_b128(
           res, (uint32_t)(p0 + 4 * ((int)threadIdx.x + kArgmaxThreads * k)) * 4u, 0, kBufNt);
+    if (p0 == 0 && wave0 && f.row_slots) {
+      slot = f.row_slots[r];
+      if (slot >= 0 && slot < f.num_slots && f.slot_eos) {
+        slot_eos = f.slot_eos[slot];
+        slot_fin = f.slot_finished[slot];
+      }
+    }
     // The pass's winner is kept as its position k * kVecElts + (EPW * j + e), a constant of
     // the unrolled loop (-1: none), and turned into an element index once per pass.
     int pos = -1;
@@ -506,16 +521,13 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
   if (lane == 0) {
     const int64_t tok = bi == 0x7fffffff ? 0 : bi;
     out[r] = tok;
-    if (f.row_slots) {
-      const int slot = f.row_slots[r];
-      if (slot >= 0 && slot < f.num_slots) {
-        if (f.slot_tokens) f.slot_tokens[slot] = tok;
-        // Rows name distinct slots within one launch (idle rows name a slot with no EOS), so the
-        // finished flag has one writer; the count is shared.
-        if (f.slot_eos && f.slot_eos[slot] >= 0 && tok == f.slot_eos[slot] && f.slot_finished[slot] == 0) {
-          f.slot_finished[slot] = 1;
-          atomicAdd(f.finished_count, 1ull);
-        }
+    if (slot >= 0 && slot < f.num_slots) {
+      if (f.slot_tokens) f.slot_tokens[slot] = tok;
+      // Rows name distinct slots within one launch (idle rows name a slot with no EOS), so the
+      // finished flag has one writer (read above, before this row's store); the count is shared.
+      if (slot_eos >= 0 && tok == slot_eos && slot_fin == 0) {
+        f.slot_finished[slot] = 1;
+        atomicAdd(f.finished_count, 1ull);
       }
     }
   }
@@ -2547,8 +2559,9 @@ int skv_gather(const void* k_pool, const void* v_pool, const int32_t* block_tabl
       hipLaunchKernelGGL(gather_rows_kernel, dim3((uint32_t)cdiv(waves, 4), v_pool ? 2 : 1), dim3(256), 0,
                          (hipStream_t)stream, (uint32_t)waves, per_row.d, per_row.m, per_head.d, per_head.m,
                          table_stride, __builtin_ctz((unsigned)block_size), __builtin_ctz((unsigned)vpr),
-                         block_tables, lens, max_len, num_blocks, num_heads, (uint32_t)pool_bytes, (const uint4*)k_pool, (const uint4*)(v_pool ? v_pool : k_pool),
-                         (uint4*)k_out, (uint4*)(v_out ? v_out : k_out));
+                         block_tables, lens, max_len, num_blocks, num_heads, (uint32_t)pool_bytes,
+                         (const uint4*)k_pool, (const uint4*)(v_pool ? v_pool : k_pool), (uint4*)k_out,
+                         (uint4*)(v_out ? v_out : k_out));
       return check_launch("skv_gather");
     }
   }
