@@ -342,7 +342,9 @@ __global__ __launch_bounds__(256) void cross_copy_kernel(CrossCopyParams p) {
 // constant; the position becomes an index once per pass). A NaN-propagating running
 // maximum (one instruction per two elements) flags a NaN, and a thread that saw one
 // rescans its elements for the first NaN (NaN counts as the maximum). A 16-bit row
-// that starts in the middle of a word has its first element handled alone.
+// that starts in the middle of a word has its first element handled alone. The
+// threads' (value, index) candidates are reduced over each wave's lanes with DPP and
+// permlane exchanges (no LDS round trip per step), then over the waves through LDS.
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxThreads = 1024;
 // 16-byte vectors per thread per pass (VECS): the launch takes the fewest of 1, 2, 4, 7 that
@@ -496,12 +498,17 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
       if ((vocab - head) & 1) consider(half_word<DT>(e[vocab - 1], 0), vocab - 1);
     }
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float v2 = __shfl_xor(best, off, 64);
-    const int i2 = __shfl_xor(bi, off, 64);
-    consider(v2, i2);
-  }
+  // (value, index) pairs reduced over lanes with DPP and permlane exchanges (every lane active).
+  auto step = [&](auto off_c) __attribute__((always_inline)) {
+    constexpr int OFF = decltype(off_c)::value;
+    consider(xor_lane<OFF>(best), __float_as_int(xor_lane<OFF>(__int_as_float(bi))));
+  };
+  step(std::integral_constant<int, 32>{});
+  step(std::integral_constant<int, 16>{});
+  step(std::integral_constant<int, 8>{});
+  step(std::integral_constant<int, 4>{});
+  step(std::integral_constant<int, 2>{});
+  step(std::integral_constant<int, 1>{});
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     s_v[wave] = best;
@@ -512,12 +519,11 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const char* __re
   const int lane = threadIdx.x;
   best = lane < kAmWaves ? s_v[lane] : kNegInf;
   bi = lane < kAmWaves ? s_i[lane] : 0x7fffffff;
-#pragma unroll
-  for (int off = kAmWaves / 2; off >= 1; off >>= 1) {
-    const float v2 = __shfl_xor(best, off, 64);
-    const int i2 = __shfl_xor(bi, off, 64);
-    consider(v2, i2);
-  }
+  static_assert(kAmWaves == 16, "the final reduction covers 16 waves");
+  step(std::integral_constant<int, 8>{});
+  step(std::integral_constant<int, 4>{});
+  step(std::integral_constant<int, 2>{});
+  step(std::integral_constant<int, 1>{});
   if (lane == 0) {
     const int64_t tok = bi == 0x7fffffff ? 0 : bi;
     out[r] = tok;
