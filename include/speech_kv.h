@@ -85,7 +85,8 @@ enum skv_status {
   SKV_EINVAL = -1,     /* bad size / null pointer / unsupported head_dim */
   SKV_EDTYPE = -2,     /* unknown dtype code */
   SKV_EALIGN = -3,     /* pointer or stride not 16-byte aligned */
-  SKV_EWORKSPACE = -4  /* workspace missing or smaller than skv_attention_workspace_bytes */
+  SKV_EWORKSPACE = -4, /* workspace missing or smaller than skv_attention_workspace_bytes */
+  SKV_EUNSUPPORTED = -5 /* skv_linear: no workspace-free hipBLASLt algorithm for the shape */
 };
 
 /* Library version string, e.g. "speechkv 0.3.0 gfx950 src:0123456789abcdef"; the
@@ -337,6 +338,23 @@ SKV_API int skv_add_layernorm(const void* x, int64_t ldx, const void* y, int64_t
 SKV_API int skv_codebook_embed_sum(const int64_t* codes, int64_t codes_stride, int32_t rows,
                                    const void* const* tables, int32_t num_codebooks, int32_t vocab,
                                    int32_t dim, void* out, int64_t out_stride, int32_t dtype, void* stream);
+
+/*
+ * skv_linear — a decode-batch projection through hipBLASLt with one plan cached per shape.
+ *   y[r*ldy + j] = sum_i x[r*ldx + i] * w[j*ldw + i] (+ bias[j]) for r < m, j < n, i < k:
+ *   row-major x [m, k], w [n, k] and y [m, n], fp32 accumulation, the result in dtype;
+ *   bias : [n] in dtype, or NULL.
+ *   The first call on a device creates its hipBLASLt handle and the first call of a shape
+ *   builds its plan (host work: make them outside graph capture). Plans use algorithms that
+ *   need no workspace, so a call allocates no device memory. SKV_EUNSUPPORTED: hipBLASLt has
+ *   no such algorithm for the shape (the caller runs its own GEMM). Calls are serialised by
+ *   a lock.
+ * Replaces the nn.Linear calls of the decoder step, speech_serving/models.py:127-207 (q/k/v,
+ * output, cross-attention and MLP projections) and :416, :486 (the LM head), whose torch
+ * dispatch rebuilds the matmul descriptors and reruns the algorithm heuristic on every call.
+ */
+SKV_API int skv_linear(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, void* y,
+                       int64_t ldy, int32_t m, int32_t n, int32_t k, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

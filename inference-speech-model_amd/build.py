@@ -19,7 +19,7 @@ PKG_ROOT = os.path.dirname(os.path.abspath(__file__))
 REPO_ROOT = os.path.dirname(PKG_ROOT)
 CSRC = os.path.join(PKG_ROOT, "csrc")
 INCLUDE = os.path.join(REPO_ROOT, "include")
-SOURCES = [os.path.join(CSRC, "skv_kernels.hip")]
+SOURCES = [os.path.join(CSRC, "skv_kernels.hip"), os.path.join(CSRC, "skv_linear.hip")]
 OUTPUT = os.path.join(PKG_ROOT, "speech_serving", "libspeechkv.so")
 ARCH = "gfx950"
 
@@ -83,6 +83,9 @@ def build(debug: bool = False, verbose: bool = False) -> str:
         "-I", CSRC,
         "-o", tmp,
         *SOURCES,
+        # skv_linear's GEMMs (loaded after torch, the library binds to torch's copy of hipBLASLt)
+        "-L", os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(hipcc()))), "lib"),
+        "-lhipblaslt",
     ]
     if verbose:
         print(" ".join(cmd), flush=True)

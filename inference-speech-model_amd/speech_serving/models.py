@@ -223,6 +223,31 @@ def _bucket_mask_lens(mask: torch.Tensor, rows: int, width: int, what: str) -> t
     return torch.where(n == 0, torch.full_like(n, width), n).to(torch.int32)
 
 
+def _hooked(mod: nn.Module) -> bool:
+    """Whether calling the module would run forward hooks (its own or global ones)."""
+    return bool(mod._forward_hooks or mod._forward_pre_hooks or nn.modules.module._global_forward_hooks or
+                nn.modules.module._global_forward_pre_hooks)
+
+
+def proj(mod: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """mod(x). A plain nn.Linear without hooks on a GPU tensor runs as one skv_linear call (a hipBLASLt plan
+    cached per shape: the algorithm and bits of torch's linear without its per-call descriptor set-up and
+    heuristic); any other module, or one with hooks, is called as usual."""
+    if x.is_cuda and type(mod) is nn.Linear and not _hooked(mod):
+        return native.linear(x, mod.weight, mod.bias)
+    return mod(x)
+
+
+def mlp(seq: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """seq(x) for the layers' Linear-GELU-Linear MLP, its projections through proj() (other modules and
+    hooked ones are called as usual)."""
+    if x.is_cuda and type(seq) is nn.Sequential and not _hooked(seq):
+        parts = tuple(seq._modules.values())
+        if len(parts) == 3 and type(parts[1]) is nn.GELU and not _hooked(parts[1]):
+            return proj(parts[2], F.gelu(proj(parts[0], x), approximate=parts[1].approximate))
+    return seq(x)
+
+
 def add_norm(x: torch.Tensor, y: Optional[torch.Tensor], norm: nn.LayerNorm) -> Tuple[torch.Tensor, torch.Tensor]:
     """(s, norm(s)) for s = x + y (s = x when y is None): one skv_add_layernorm launch
     on the GPU, the same two torch ops elsewhere."""
@@ -300,17 +325,17 @@ class DecoderLayer(nn.Module):
         """q, k, v [B, S, H, D] from the already normalised input h."""
         b, s, _ = h.shape
         hd = self.num_heads * self.head_dim
-        qkv = F.linear(h, self.qkv_weight())
+        qkv = native.linear(h, self.qkv_weight()) if h.is_cuda else F.linear(h, self.qkv_weight())
         shape = (b, s, self.num_heads, self.head_dim)
         return qkv[..., :hd].view(shape), qkv[..., hd:2 * hd].view(shape), qkv[..., 2 * hd:].view(shape)
 
     def _finish(self, x: torch.Tensor, cross_used: bool) -> torch.Tensor:
         norm = self.norm3 if cross_used else self.norm2
-        return x + self.mlp(norm(x))
+        return x + mlp(self.mlp, norm(x))
 
     def _cross_q(self, x: torch.Tensor) -> torch.Tensor:
         b, s, _ = x.shape
-        return self.cross_attn_q(self.norm2(x)).view(b, s, self.num_heads, self.head_dim)
+        return proj(self.cross_attn_q, self.norm2(x)).view(b, s, self.num_heads, self.head_dim)
 
     # -- paged hot path ---------------------------------------------------------
     def forward_paged(self, x: torch.Tensor, layer: int, kv: PagedKV, cross: Optional[CrossKV],
@@ -326,17 +351,17 @@ class DecoderLayer(nn.Module):
         attn = native.paged_attention(q, kv.k_pools[layer], kv.v_pools[layer], kv.block_tables, kv.ctx_lens,
                                       kv.max_ctx, self.scale, causal=s > 1, table_rows=kv.table_rows,
                                       k_new=k, v_new=v, rows_longest_first=kv.rows_longest_first)
-        a = self.self_attn_out(attn.view(b, s, hd))
+        a = proj(self.self_attn_out, attn.view(b, s, hd))
         used = cross is not None and cross.has(layer)
         if used:
             x, h = add_norm(x, a, self.norm2)
-            cq = self.cross_attn_q(h).view(b, s, self.num_heads, self.head_dim)
+            cq = proj(self.cross_attn_q, h).view(b, s, self.num_heads, self.head_dim)
             c = native.dense_attention(cq, cross.k[layer], cross.v[layer], cross.lens,
                                        cross.max_len, self.scale, slot_ids=cross.slot_ids)
-            x, h = add_norm(x, self.cross_attn_out(c.view(b, s, hd)), self.norm3)
+            x, h = add_norm(x, proj(self.cross_attn_out, c.view(b, s, hd)), self.norm3)
         else:
             x, h = add_norm(x, a, self.norm2)
-        return x, self.mlp(h)
+        return x, mlp(self.mlp, h)
 
     # -- contiguous API of the reference (models.py:110-208) ---------------------
     def forward(self, x: torch.Tensor, past_key_values: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
@@ -363,7 +388,7 @@ class DecoderLayer(nn.Module):
             kk, vv = k, v
             lens = torch.full((b,), t, dtype=torch.int32, device=x.device)
         attn = native.dense_attention(q, kk, vv, lens, t, self.scale, causal=self.is_decoder and s > 1)
-        x = x + self.self_attn_out(attn.reshape(b, s, hd))
+        x = x + proj(self.self_attn_out, attn.reshape(b, s, hd))
 
         new_cross = None
         used = encoder_hidden_states is not None or encoder_past_kv is not None
@@ -387,7 +412,7 @@ class DecoderLayer(nn.Module):
             if ck.shape[0] == 1 and b > 1:
                 ck, cv = ck.expand(b, -1, -1, -1), cv.expand(b, -1, -1, -1)
             c = native.dense_attention(self._cross_q(x), ck, cv, clens, te, self.scale)
-            x = x + self.cross_attn_out(c.reshape(b, s, hd))
+            x = x + proj(self.cross_attn_out, c.reshape(b, s, hd))
         return self._finish(x, used), new_past, new_cross
 
 
@@ -479,7 +504,7 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
             x = x[:, -1]
             pending = None if pending is None else pending[:, -1]
         _, h = add_norm(x, pending, self.decoder_norm)
-        return self.lm_head(h)
+        return proj(self.lm_head, h)
 
     # -- decode step, reference signature (models.py:369-423) ----------------------------
     def decode_step(self, input_ids: torch.Tensor, past_key_values: Optional[Any] = None,
@@ -521,7 +546,7 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
         keep = int(kwargs.get("logits_to_keep", 0) or 0)
         if keep > 0:
             x = x[:, -keep:]
-        return ModelOutput(self.lm_head(self.decoder_norm(x)), cache)
+        return ModelOutput(proj(self.lm_head, self.decoder_norm(x)), cache)
 
     def _decode_step_paged_cache(self, input_ids: torch.Tensor, cache: PagedKVCache,
                                  encoder_past_kv_list: Optional[List[Tuple[torch.Tensor, torch.Tensor]]],
@@ -621,7 +646,7 @@ class WhisperClassSpeechEncoderDecoderModel(nn.Module):
                                        t_enc, layer.scale)
             x = x + layer.cross_attn_out(c.view(max_slots, 1, hd))
             x = layer._finish(x, True)
-        logits = self.lm_head(self.decoder_norm(x[:, -1, :]))
+        logits = proj(self.lm_head, self.decoder_norm(x[:, -1, :]))
         native.argmax(logits, out=g_output_tokens)
 
 
@@ -670,7 +695,9 @@ class MultiCodebookHeads(nn.Module):
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         """[B, S, hidden] -> logits [B, S, K, V]."""
         b, s, _ = hidden_states.shape
-        return F.linear(hidden_states, self.fused_weight()).view(b, s, self.num_codebooks, self.vocab_size)
+        w = self.fused_weight()
+        y = native.linear(hidden_states, w) if hidden_states.is_cuda else F.linear(hidden_states, w)
+        return y.view(b, s, self.num_codebooks, self.vocab_size)
 
 
 class StreamingMultiCodebookTTSModel(nn.Module):

@@ -9,6 +9,8 @@ Functions:
     gather(k_pool, v_pool, block_tables, lens, max_len)
     paged_attention(q, k_pool, v_pool, block_tables, ctx_lens, max_ctx, scale, ...)
     dense_attention(q, k, v, lens, max_len, scale, ...)
+    argmax(logits, ...), copy_cross_kv(...), add_layernorm(...), codebook_embed_sum(...)
+    linear(x, weight, bias)   (hipBLASLt with a plan cached per shape)
 """
 from __future__ import annotations
 
@@ -57,7 +59,9 @@ SIGNATURES = {
                                    _c_i32, _c_i32, _c_i32, _c_p]),
     "skv_codebook_embed_sum": (_c_int, [_c_p, _c_i64, _c_i32, _c_p, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32,
                                         _c_p]),
+    "skv_linear": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),
 }
+SKV_EUNSUPPORTED = -5  # skv_linear: no workspace-free hipBLASLt algorithm for the shape
 MAX_CODEBOOKS = 16  # kMaxCodebooks of the library
 
 
@@ -574,6 +578,39 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: tor
         1 if causal else 0, _code(q4.dtype), chunk_tokens, wp, wn, _stream(q.device))
     _check(rc, "skv_dense_attention")
     return out
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x @ weight.T (+ bias): x [..., k], weight [n, k] with contiguous rows, bias [n], one dtype, on the GPU.
+
+    One skv_linear call: a hipBLASLt plan cached per shape, where torch's linear rebuilds its descriptors
+    and reruns the algorithm heuristic on every call. At the decode shapes the algorithm (and so every
+    bit of the result) is the one torch's linear runs. Where hipBLASLt has no workspace-free algorithm for
+    the shape, torch's linear runs instead. Reference: the nn.Linear projections of
+    speech_serving/models.py:127-207 and the LM head (:416, :486).
+    """
+    k = x.shape[-1]
+    if not x.is_cuda or not weight.is_cuda:
+        raise RuntimeError("linear: x and weight must be GPU tensors; the HIP path has no CPU variant")
+    code = _DTYPE_CODE.get(x.dtype)
+    if code is None or weight.dtype != x.dtype or weight.dim() != 2 or weight.shape[1] != k or weight.stride(1) != 1:
+        raise RuntimeError(f"linear: weight {tuple(weight.shape)} {weight.dtype} does not fit x [..., {k}] {x.dtype}")
+    n = weight.shape[0]
+    if bias is not None and (bias.dtype != x.dtype or bias.dim() != 1 or bias.shape[0] != n or bias.stride(0) != 1
+                             or not bias.is_cuda):
+        raise RuntimeError(f"linear: bias must be a contiguous GPU [{n}] {x.dtype} vector")
+    x2 = x.reshape(-1, k)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    y = torch.empty(x.shape[:-1] + (n,), dtype=x.dtype, device=x.device)
+    rc = lib().skv_linear(x2.data_ptr(), x2.stride(0) if m > 1 else k, weight.data_ptr(),
+                          weight.stride(0) if n > 1 else k, None if bias is None else bias.data_ptr(),
+                          y.data_ptr(), n, m, n, k, code, _stream(x.device))
+    if rc == SKV_EUNSUPPORTED:
+        return torch.nn.functional.linear(x, weight, bias)
+    _check(rc, "skv_linear")
+    return y
 
 
 def add_layernorm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
