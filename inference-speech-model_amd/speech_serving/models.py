@@ -251,9 +251,12 @@ def mlp(seq: nn.Module, x: torch.Tensor) -> torch.Tensor:
 def add_norm(x: torch.Tensor, y: Optional[torch.Tensor], norm: nn.LayerNorm) -> Tuple[torch.Tensor, torch.Tensor]:
     """(s, norm(s)) for s = x + y (s = x when y is None): one skv_add_layernorm launch
     on the GPU, the same two torch ops elsewhere."""
-    if x.is_cuda and norm.elementwise_affine and norm.bias is not None and \
-            native.add_layernorm_supported(x, norm.weight):
-        return native.add_layernorm(x, y, norm.weight, norm.bias, norm.eps)
+    if x.is_cuda and norm.elementwise_affine and not _hooked(norm):
+        bias = norm.bias
+        if bias is not None:
+            got = native.add_layernorm(x, y, norm.weight, bias, norm.eps, fallback=True)
+            if got is not None:
+                return got
     s = x if y is None else x + y
     return s, norm(s)
 

@@ -500,7 +500,7 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     code = _code(q4.dtype)
     max_ctx = max(0, min(int(max_ctx), block_tables.shape[1] * bs))
     if chunk_tokens <= 0:
-        chunk_tokens = paged_chunk_tokens(bsz * qlen, heads, hkv, d, max(max_ctx, 1), q4.dtype, bs, nb)
+        chunk_tokens = _paged_chunk(bsz * qlen, heads, hkv, d, max(max_ctx, 1), code, bs, nb)
     kn4 = vn4 = None
     nstr = (0, 0, 0)
     if (k_new is None) != (v_new is None):
@@ -525,7 +525,7 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     if noalloc:
         _check(lib().skv_paged_attention_noalloc(*args, _stream(q.device)), "skv_paged_attention_noalloc")
         return out
-    need = attention_workspace_bytes(bsz * qlen, heads, d, max_ctx, q4.dtype, chunk_tokens)
+    need = _workspace_bytes(bsz * qlen, heads, d, max_ctx, chunk_tokens, code)
     wp, wn = _scratch(need, q.device)
     _check(lib().skv_paged_attention(*args, wp, wn, _stream(q.device)), "skv_paged_attention")
     return out
@@ -567,15 +567,16 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, lens: tor
     if tuple(o4.shape) != tuple(q4.shape) or o4.stride(3) != 1:
         raise RuntimeError("dense_attention: out must match q's shape with contiguous head_dim")
     max_len = max(0, min(int(max_len), tmax))
+    code = _code(q4.dtype)
     if chunk_tokens <= 0:
-        chunk_tokens = default_chunk_tokens(bsz * qlen, heads, d, max(max_len, 1), q4.dtype)
-    need = attention_workspace_bytes(bsz * qlen, heads, d, max_len, q4.dtype, chunk_tokens)
+        chunk_tokens = _default_chunk(bsz * qlen, heads, d, max(max_len, 1), code)
+    need = _workspace_bytes(bsz * qlen, heads, d, max_len, chunk_tokens, code)
     wp, wn = _scratch(need, q.device)
     rc = lib().skv_dense_attention(
         q4.data_ptr(), q4.stride(0), q4.stride(1), q4.stride(2), k.data_ptr(), v.data_ptr(),
         k.stride(0), k.stride(1), k.stride(2), _ptr(slot_ids), lens.data_ptr(), o4.data_ptr(),
         o4.stride(0), o4.stride(1), o4.stride(2), bsz, qlen, heads, hkv, d, max_len, float(scale),
-        1 if causal else 0, _code(q4.dtype), chunk_tokens, wp, wn, _stream(q.device))
+        1 if causal else 0, code, chunk_tokens, wp, wn, _stream(q.device))
     _check(rc, "skv_dense_attention")
     return out
 
@@ -616,31 +617,45 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
 def add_layernorm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
     """Whether skv_add_layernorm takes this LayerNorm: a GPU tensor of a supported dtype whose
     hidden size is a multiple of the 16-byte vector (and at most 512 vectors), with 16-byte rows."""
-    if not x.is_cuda or x.dtype not in _DTYPE_CODE or weight.dtype != x.dtype:
-        return False
+    return _layernorm_rows(x, weight) is not None
+
+
+def _layernorm_rows(x: torch.Tensor, weight: torch.Tensor):
+    """(x as [rows, hidden], hidden, 16-byte vectors per element count) when skv_add_layernorm takes x
+    with this weight, else None."""
+    if not x.is_cuda or weight.dtype != x.dtype or x.dtype not in _DTYPE_CODE or x.stride(-1) != 1:
+        return None
     h = x.shape[-1]
     epl = 16 // x.element_size()
-    if h % epl or h > 512 * epl or x.stride(-1) != 1:
-        return False
-    rows = x.numel() // h if h else 0
-    x2 = x.reshape(rows, h) if rows else x
-    return rows == 0 or (x2.stride(0) % epl == 0 and x2.data_ptr() % 16 == 0)
+    if h == 0 or h % epl or h > 512 * epl:
+        return None
+    x2 = x.reshape(-1, h)
+    if x2.shape[0] and (x2.stride(0) % epl or x2.data_ptr() % 16):
+        return None
+    return x2, h, epl
 
 
 def add_layernorm(x: torch.Tensor, y: Optional[torch.Tensor], weight: torch.Tensor, bias: torch.Tensor,
-                  eps: float, sum_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                  eps: float, sum_out: Optional[torch.Tensor] = None,
+                  fallback: bool = False) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
     """(s, LayerNorm(s)) with s = x + y rounded to x's dtype (s = x when y is None).
 
-    x, y [..., hidden]; weight, bias [hidden]. sum_out may be x (in-place residual).
+    x, y [..., hidden]; weight, bias [hidden]. sum_out may be x (in-place residual). An x the kernel
+    does not take (a CPU tensor, another dtype, a hidden size that is not a multiple of the 16-byte
+    vector or above 512 of them, rows that are not 16-byte aligned, a weight or bias of another size)
+    raises RuntimeError, or with fallback=True returns None (the caller then runs torch's ops).
     """
-    _gpu(x, "x")
-    h = x.shape[-1]
-    epl = 16 // x.element_size()
-    rows = x.numel() // h if h else 0
-    x2 = x.reshape(rows, h) if rows else x
-    if x.dtype not in _DTYPE_CODE or weight.dtype != x.dtype or h % epl or h > 512 * epl or x.stride(-1) != 1 or \
-            (rows and (x2.stride(0) % epl or x2.data_ptr() % 16)):
-        raise RuntimeError("add_layernorm: unsupported dtype/hidden size/layout")
+    got = _layernorm_rows(x, weight)
+    if got is not None and (not weight.is_contiguous() or weight.numel() != got[1] or bias.dtype != x.dtype or
+                            not bias.is_contiguous() or bias.numel() != got[1]):
+        got = None
+    if got is None:
+        if fallback:
+            return None
+        _gpu(x, "x")
+        raise RuntimeError("add_layernorm: unsupported dtype, hidden size, layout or weight/bias shape")
+    x2, h, epl = got
+    rows = x2.shape[0]
     y2 = None
     if y is not None:
         _gpu(y, "y")
@@ -651,15 +666,12 @@ def add_layernorm(x: torch.Tensor, y: Optional[torch.Tensor], weight: torch.Tens
             sum_out = torch.empty_like(x)
     s2 = sum_out.reshape(rows, h) if sum_out is not None else None
     norm = torch.empty(x.shape, dtype=x.dtype, device=x.device)
-    n2 = norm.view(rows, h)
-    for t, name in ((weight, "weight"), (bias, "bias")):
-        if not t.is_contiguous() or t.numel() != h or t.dtype != x.dtype:
-            raise RuntimeError(f"add_layernorm: {name} must be contiguous [hidden] in x's dtype")
-    ld = lambda t: t.stride(0) if rows > 1 else h  # noqa: E731
-    rc = lib().skv_add_layernorm(x2.data_ptr(), ld(x2), _ptr(y2), ld(y2) if y2 is not None else h,
+    many = rows > 1
+    rc = lib().skv_add_layernorm(x2.data_ptr(), x2.stride(0) if many else h, _ptr(y2),
+                                 y2.stride(0) if many and y2 is not None else h,
                                  weight.data_ptr(), bias.data_ptr(), float(eps),
-                                 _ptr(s2), ld(s2) if s2 is not None else h, n2.data_ptr(), h, rows, h,
-                                 _code(x.dtype), _stream(x.device))
+                                 _ptr(s2), s2.stride(0) if many and s2 is not None else h, norm.data_ptr(), h, rows,
+                                 h, _DTYPE_CODE[x.dtype], _stream(x.device))
     _check(rc, "skv_add_layernorm")
     return (sum_out if y is not None else x), norm
 
