@@ -102,8 +102,11 @@ SKV_API const char* skv_last_error(void);
  *   k_new, v_new : [N, H, D] rows (row stride new_stride_n, head stride new_stride_h)
  *   k_pool,v_pool: [num_blocks, block_size, H, D], contiguous
  *   slot_mapping : int64 [N] device; slot = block_id * block_size + offset;
- *                  a negative slot skips that row.
+ *                  a negative slot, or one at or past num_slots, skips that row.
  * Either v_new/v_pool pair may be NULL to append K only.
+ * Rows that name the same slot in one call race (the slot ends up holding one of
+ * them, not necessarily the last); the reference's writes name distinct slots
+ * (each request its own next positions).
  * Reference: phase_aware_scheduler.py:1004-1010 (decode), :681-690 (prefill).
  */
 SKV_API int skv_append(const void* k_new, const void* v_new,
