@@ -601,9 +601,9 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
                              or not bias.is_cuda):
         raise RuntimeError(f"linear: bias must be a contiguous GPU [{n}] {x.dtype} vector")
     x2 = x.reshape(-1, k)
-    if x2.stride(1) != 1:
-        x2 = x2.contiguous()
     m = x2.shape[0]
+    if x2.stride(1) != 1 or (m > 1 and x2.stride(0) < k):  # e.g. rows broadcast from one (stride 0)
+        x2 = x2.contiguous()
     y = torch.empty(x.shape[:-1] + (n,), dtype=x.dtype, device=x.device)
     rc = lib().skv_linear(x2.data_ptr(), x2.stride(0) if m > 1 else k, weight.data_ptr(),
                           weight.stride(0) if n > 1 else k, None if bias is None else bias.data_ptr(),

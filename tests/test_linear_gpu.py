@@ -69,6 +69,8 @@ def test_linear_strided_rows_batch_dims_and_empty(cuda):
     y3 = native.linear(x3, w, b)
     assert y3.shape == (4, 6, 512) and torch.equal(y3.view(24, 512), native.linear(x, w, b))
     assert native.linear(x[:0], w, b).shape == (0, 512)
+    xb = x[:1].expand(24, 256)  # rows broadcast from one (row stride 0)
+    assert torch.equal(native.linear(xb, w, b), F.linear(xb.contiguous(), w, b))
 
 
 def test_linear_graph_replays_equal_eager(cuda):
