@@ -131,12 +131,16 @@ class PagedKVCache:
 
     cross_lens / cross_mask: the batch's encoder lengths (int32 [B] on the device) and the
     encoder_attention_mask built from them. decode_step takes the lengths as they are when
-    it receives that same mask object, and derives them from any other mask."""
+    it receives that same mask object, and derives them from any other mask.
+    rows_longest_first: the caller knows ctx_lens to be non-increasing (the attention launch
+    then skips ranking the rows by length; results are the same either way)."""
 
     def __init__(self, k_pools: Sequence[torch.Tensor], v_pools: Sequence[torch.Tensor], block_tables: torch.Tensor,
                  ctx_lens: torch.Tensor, max_ctx: int, table_rows: Optional[torch.Tensor] = None,
-                 cross_lens: Optional[torch.Tensor] = None, cross_mask: Optional[torch.Tensor] = None):
+                 cross_lens: Optional[torch.Tensor] = None, cross_mask: Optional[torch.Tensor] = None,
+                 rows_longest_first: bool = False):
         self.k_pools, self.v_pools = k_pools, v_pools
+        self.rows_longest_first = bool(rows_longest_first)
         self.block_tables, self.ctx_lens, self.max_ctx = block_tables, ctx_lens, int(max_ctx)
         self.table_rows = table_rows
         self.cross_lens, self.cross_mask = cross_lens, cross_mask
@@ -147,7 +151,8 @@ class PagedKVCache:
         return len(self.layers)
 
     def paged(self) -> "PagedKV":
-        return PagedKV(self.k_pools, self.v_pools, self.block_tables, self.ctx_lens, self.max_ctx, self.table_rows)
+        return PagedKV(self.k_pools, self.v_pools, self.block_tables, self.ctx_lens, self.max_ctx, self.table_rows,
+                       self.rows_longest_first)
 
 
 @dataclass

@@ -716,8 +716,10 @@ class PhaseAwareSpeechScheduler:
         enc_mask = self._encoder_mask(enc_lens, enc)
         with torch.no_grad():
             if self._paged_model:
-                cache = PagedKVCache(dec_bm.key_pool, dec_bm.value_pool, tables, ctx, int(meta[:, maxblk].max()),
-                                     cross_lens=enc, cross_mask=enc_mask)
+                lens = meta[:, maxblk]
+                cache = PagedKVCache(dec_bm.key_pool, dec_bm.value_pool, tables, ctx, int(lens.max()),
+                                     cross_lens=enc, cross_mask=enc_mask,
+                                     rows_longest_first=bool((lens[1:] <= lens[:-1]).all()))
                 out = self.model.decode_step(input_ids=ids, past_key_values=cache, encoder_past_kv_list=enc_list,
                                              attention_mask=None, encoder_attention_mask=enc_mask, position_ids=pos,
                                              use_cache=True, logits_to_keep=1)

@@ -177,7 +177,8 @@ class StreamingTTSEngine:
         rows = [t + [0] * (width - len(t)) for t in tables]  # padding past a row's keys is never read
         dev = bm.key_pool[0].device
         return PagedKVCache(bm.key_pool, bm.value_pool, torch.tensor(rows, dtype=torch.int32).to(dev),
-                            torch.tensor(ctx, dtype=torch.int32).to(dev), max(ctx))
+                            torch.tensor(ctx, dtype=torch.int32).to(dev), max(ctx),
+                            rows_longest_first=all(a >= b for a, b in zip(ctx, ctx[1:])))
 
     @torch.no_grad()
     def _prefill(self, req: TTSRequest) -> torch.Tensor:
