@@ -3,7 +3,7 @@
 - roofline.traffic comes from the committed rocprofv3 summary only for the same workload and a library built from
   the same sources (the source digest); any other digest, workload or a forced chunk gives null;
 - the algorithmic bytes of a paged attention launch (K/V of every context, q, out, table entries, lengths);
-- the ctypes binding in INTEGRATION.md passes as many arguments as include/speech_kv.h declares."""
+- the ctypes binding shown in the integration guide passes as many arguments as include/speech_kv.h declares."""
 import argparse
 import math
 import os
@@ -59,5 +59,5 @@ def test_integration_binding_matches_the_header():
     declared = header[i + len("skv_paged_attention("):header.index(");", i)].count(",") + 1
     doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     m = re.search(r"_lib\.skv_paged_attention\.argtypes = \[(.*?)\]\n", doc, re.S)
-    assert m, "INTEGRATION.md no longer shows the skv_paged_attention binding"
+    assert m, "the integration guide no longer shows the skv_paged_attention binding"
     assert len([x for x in m.group(1).split(",") if x.strip()]) == declared
