@@ -200,3 +200,22 @@ def test_cross_arena_keeps_live_requests_in_the_leading_slots():
     # batches split where the slots stop being consecutive
     rs = [SimpleNamespace(s=s) for s in (4, 0, 1, 3, 7, 2)]
     assert [[r.s for r in run] for run in _slot_runs(rs, lambda r: r.s)] == [[0, 1, 2, 3, 4], [7]]
+
+
+def test_projection_helpers_call_modules_off_the_gpu():
+    """On CPU tensors the decode step's projection, MLP and add+LayerNorm helpers run the modules and torch ops
+    (the library's GEMM and LayerNorm launches are for GPU tensors only)."""
+    import torch.nn as nn
+
+    from speech_serving import models
+
+    torch.manual_seed(0)
+    lin = nn.Linear(16, 8)
+    x = torch.randn(3, 16)
+    assert torch.equal(models.proj(lin, x), lin(x))
+    seq = nn.Sequential(nn.Linear(16, 32), nn.GELU(), nn.Linear(32, 16))
+    assert torch.equal(models.mlp(seq, x), seq(x))
+    norm = nn.LayerNorm(16)
+    y = torch.randn(3, 16)
+    s, n = models.add_norm(x, y, norm)
+    assert torch.equal(s, x + y) and torch.equal(n, norm(x + y))
